@@ -1,0 +1,50 @@
+"""ctypes binding of libf16acc_amd.so (the C ABI in include/f16acc.h).
+
+There is no fallback: if the library is missing, importing this module
+raises, and the package cannot be used.
+"""
+
+import ctypes
+import os
+
+from .build import LIB
+
+if not os.path.exists(LIB):
+    raise ImportError(f"{LIB} is not built; run `python f16acc_amd/build.py` (needs hipcc for gfx950)")
+
+_dll = ctypes.CDLL(LIB)
+
+_i64, _vp, _int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int
+_P64 = ctypes.POINTER(ctypes.c_int64)
+_PI = ctypes.POINTER(ctypes.c_int)
+
+gemm = _dll.f16acc_gemm
+gemm.argtypes = [_vp, _vp, _vp, _vp] + [_i64] * 9 + [_int, _int, _vp]
+gemm.restype = _int
+
+tile_config = _dll.f16acc_tile_config
+tile_config.argtypes = [_i64] * 7 + [_vp, _vp, _PI, _PI, _P64, _P64, _PI, _PI]
+tile_config.restype = _int
+
+block_tile = _dll.f16acc_block_tile
+block_tile.argtypes = [_i64, _i64, _i64, _P64, _P64]
+block_tile.restype = _int
+
+strerror = _dll.f16acc_strerror
+strerror.argtypes = [_int]
+strerror.restype = ctypes.c_char_p
+
+abi_version = _dll.f16acc_abi_version
+abi_version.argtypes = []
+abi_version.restype = _int
+
+# Exported symbol names, as declared in include/f16acc.h.
+EXPORTS = ("f16acc_gemm", "f16acc_tile_config", "f16acc_block_tile", "f16acc_strerror", "f16acc_abi_version")
+
+OUT_F16, OUT_F32 = 0, 1
+E_ARG, E_UNSUPPORTED = -1, -2
+
+
+def check(rc):
+    if rc != 0:
+        raise RuntimeError(strerror(rc).decode())

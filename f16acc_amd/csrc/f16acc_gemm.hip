@@ -1,0 +1,571 @@
+// Chunked FP16 GEMM for MI355X (gfx950 / CDNA4).
+//
+// c[M,N] = a[M,K] @ b[K,N]; binary16 operands, binary16 or binary32 output.
+// Chunked mode keeps the reference's numerics (f16acc/kernel.py:37-81):
+// every 32-long K chunk of a dot product is summed, rounded once to binary16
+// (round to nearest even, overflow to inf) and added to an FP32 running sum;
+// an output tile whose FP32 sum ends up inf/NaN is recomputed, whole, with
+// FP32 accumulation by the same workgroup, so there is no second launch and
+// no host sync.
+//
+// gfx950 has no FP16-accumulating MFMA, so the chunk is one
+// v_mfma_f32_16x16x32_f16 with a zero accumulator (K = 32 = one chunk), and
+// the rounding is done in the epilogue of each MFMA pair:
+//   v_cvt_pk_f16_f32  packs the partials of two consecutive chunks of the
+//                     same element into one register (RNE, inf past 65504)
+//   v_dot2_f32_f16    adds both halves into the FP32 sum (x*1 + y*1 + s)
+// i.e. one VALU instruction per output element per chunk next to 64 MFMA
+// flops, which a 16x16x32 MFMA (16 cycles for 256 elements) and the VALU
+// (4 cycles per wave64 instruction) can overlap.
+//
+// Data path per workgroup: operand tiles are staged global -> LDS with
+// buffer_load_dwordx4 ... lds (no VGPR round trip), 64 K (two chunks) per
+// stage, two stages in flight.  Out-of-range 16-byte units (M/N/K edges) are
+// zero-filled by the buffer range check, like the reference's masked loads
+// (kernel.py:45-47).  LDS layouts:
+//   KC  (operand K-contiguous: a row-major, or b given as w.t()):
+//       row r holds its 64 k as eight 16-byte units, unit u stored at
+//       position u ^ kc_swz(r); MFMA fragments are ds_read_b128.
+//   NC  (b N-contiguous, row-major [K, N]):
+//       k-row holds BN n as BN/8 units, unit u stored at u ^ nc_swz(k);
+//       fragments are ds_read_b64_tr_b16 (LDS transpose read).
+// Operands whose strides or alignment do not fit these paths go through a
+// generic kernel that gathers elements through registers into the KC layout.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "f16acc.h"
+
+namespace {
+
+typedef _Float16 f16;
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+#define LDS_AS __attribute__((address_space(3)))
+
+constexpr int kChunk = 32;      // reference BLOCK_K (kernel.py:17): the rounding interval
+constexpr int kStageK = 64;     // K per LDS stage: two chunks, paired by v_dot2
+constexpr int kNumXcd = 8;      // MI355X: workgroups are dealt round-robin over 8 XCDs
+constexpr int kGroupM = 8;      // group-M swizzle width (reference G = 8, kernel.py:17)
+constexpr int kOob = 0x7fffff00;  // buffer offset past num_records: the load returns 0
+
+static_assert(kStageK == 2 * kChunk, "a stage holds exactly one chunk pair");
+
+struct Params {
+  const f16* a;
+  const f16* b;
+  void* c;
+  uint8_t* flags;
+  int64_t M, N, K;
+  int64_t sam, sak, sbk, sbn, scm, scn;
+  int64_t tiles_m, tiles_n;
+  int vec_store;  // c rows are contiguous and 16-byte aligned in 4-element groups
+};
+
+// ---------------------------------------------------------------------------
+// Workgroup -> output tile.  Workgroups are dispatched round-robin over the
+// XCDs (block b runs on XCD b % 8) and each XCD has its own L2, so blocks are
+// first renumbered so that every XCD owns one contiguous range of logical
+// tile ids, then the range is laid out group-M (kGroupM tile rows at a time,
+// column-major inside a group, as the reference's _tile does,
+// kernel.py:26-29) so one XCD's tiles share A rows and B columns.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline void block_tile(int64_t block, int64_t tiles_m, int64_t tiles_n,
+                                           int64_t* tm, int64_t* tn) {
+  const int64_t total = tiles_m * tiles_n;
+  const int64_t x = block % kNumXcd, l = block / kNumXcd;
+  const int64_t q = total / kNumXcd, r = total % kNumXcd;
+  const int64_t id = x < r ? x * (q + 1) + l : r * (q + 1) + (x - r) * q + l;
+  const int64_t width = kGroupM * tiles_n;
+  const int64_t first = (id / width) * kGroupM;
+  const int64_t gsz = tiles_m - first < kGroupM ? tiles_m - first : kGroupM;
+  *tm = first + (id % width) % gsz;
+  *tn = (id % width) / gsz;
+}
+
+// LDS swizzles (see the header comment).  kc_swz spreads the 16 rows one
+// ds_read_b128 touches over distinct 16-byte bank groups; nc_swz does the
+// same for the 4 k-rows x 2 units each 16-lane group of a transpose read
+// touches, and for the two lane groups one LDS cycle may serve together.
+__device__ __forceinline__ int kc_swz(int row) { return ((row >> 1) ^ ((row & 1) << 2)) & 7; }
+__device__ __forceinline__ int nc_swz(int krow) { return 2 * (krow & 3) + 8 * ((krow >> 3) & 1); }
+
+// Layout of B in LDS.
+enum BLayout { kKC = 0, kNC = 1 };
+
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int BL_>
+struct Cfg {
+  static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, BL = BL_;
+  static constexpr int T = 64 * WAVES_M * WAVES_N;
+  static constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;  // wave tile
+  static constexpr int FM = WTM / 16, FN = WTN / 16;            // 16x16 MFMA blocks per wave
+  static constexpr int A_STAGE = BM * kStageK * 2;               // bytes
+  static constexpr int B_STAGE = BN * kStageK * 2;
+  static constexpr int STAGE = A_STAGE + B_STAGE;
+  static constexpr int LA = BM * 8 / T;                          // 16-byte units per thread per stage
+  static constexpr int LB = BN * 8 / T;
+  static constexpr int UB = BN / 8;                              // NC: units per k-row
+  static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave tile must be whole 16x16 blocks");
+  static_assert(BM * 8 % T == 0 && BN * 8 % T == 0, "stage must split evenly over threads");
+  static_assert(BL == kKC || BN >= 128, "NC swizzle needs at least 16 units per k-row");
+};
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer resource for a raw byte window starting at `base`: stride 0,
+// num_records kOob, word 3 = 0x00020000 (gfx9 untyped 32-bit data).
+__device__ __forceinline__ i32x4 make_srd(const void* base) {
+  const uint64_t addr = (uint64_t)base;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)addr);
+  r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(addr >> 32));
+  r[2] = kOob;
+  r[3] = 0x00020000;
+  return r;
+}
+
+// One 16-byte global -> LDS copy per lane: lane i writes LDS bytes
+// [lds + 16 i, lds + 16 i + 16).  Issued as asm so the compiler does not
+// treat it as a store to every LDS buffer and wait for it before unrelated
+// ds_reads; the loop waits for it explicitly (wait_vm0 + barrier) before the
+// stage it fills is read.  M0 carries the LDS address; one wait state is
+// required between writing M0 and the DMA that reads it.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved: the asm sets it itself
+__device__ __forceinline__ void lds_dma16(const i32x4& srd, int lds, int voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(lds), "v"(voff), "s"(srd)
+      : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ void wait_vm0() {
+  // s_waitcnt vmcnt(0), other counters left alone (gfx9 encoding)
+  __builtin_amdgcn_s_waitcnt(0x0f70);
+}
+
+// ---------------------------------------------------------------------------
+// Per-thread stage loader state for the direct-to-LDS fast path.
+// ---------------------------------------------------------------------------
+template <class C>
+struct FastLoader {
+  int a_off[C::LA];   // byte offset inside the stage's rebased A window (or kOob)
+  int a_k[C::LA];     // first k of the unit (relative to the stage)
+  int b_off[C::LB];
+  int b_k[C::LB];     // KC: first k of the unit; NC: k-row of the unit
+
+  __device__ void init(const Params& p, int64_t m0, int64_t n0, int tid) {
+#pragma unroll
+    for (int j = 0; j < C::LA; ++j) {
+      const int s = j * C::T + tid, row = s >> 3, u = (s & 7) ^ kc_swz(row);
+      a_off[j] = (m0 + row < p.M) ? (int)(row * p.sam * 2 + u * 16) : kOob;
+      a_k[j] = 8 * u;
+    }
+#pragma unroll
+    for (int j = 0; j < C::LB; ++j) {
+      const int s = j * C::T + tid;
+      if (C::BL == kKC) {
+        const int row = s >> 3, u = (s & 7) ^ kc_swz(row);
+        b_off[j] = (n0 + row < p.N) ? (int)(row * p.sbn * 2 + u * 16) : kOob;
+        b_k[j] = 8 * u;
+      } else {
+        const int krow = s / C::UB, u = (s % C::UB) ^ (nc_swz(krow) & (C::UB - 1));
+        b_off[j] = (n0 + 8 * u < p.N) ? (int)(krow * p.sbk * 2 + u * 16) : kOob;
+        b_k[j] = krow;
+      }
+    }
+  }
+
+  // Issue the global -> LDS copies of the stage starting at k = kbase.
+  __device__ void issue(const Params& p, int64_t m0, int64_t n0, int64_t kbase, char LDS_AS* stage,
+                        int wave) {
+    const int64_t krem = p.K - kbase;  // k < krem is inside the matrix
+    const i32x4 ra = make_srd(p.a + (m0 * p.sam + kbase));
+    const i32x4 rb = C::BL == kKC ? make_srd(p.b + (n0 * p.sbn + kbase)) : make_srd(p.b + (kbase * p.sbk + n0));
+    const int lds = __builtin_amdgcn_readfirstlane((int)(uint32_t)(size_t)stage + wave * 64 * 16);
+#pragma unroll
+    for (int j = 0; j < C::LA; ++j) lds_dma16(ra, lds + j * C::T * 16, a_k[j] < krem ? a_off[j] : kOob);
+#pragma unroll
+    for (int j = 0; j < C::LB; ++j)
+      lds_dma16(rb, lds + C::A_STAGE + j * C::T * 16, b_k[j] < krem ? b_off[j] : kOob);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Compute one 64-K stage out of LDS into the wave's accumulators.
+// ---------------------------------------------------------------------------
+template <class C>
+__device__ __forceinline__ f16x8 read_kc(const char LDS_AS* base, int row, int u) {
+  return *(const f16x8 LDS_AS*)(base + row * (kStageK * 2) + ((u ^ kc_swz(row)) << 4));
+}
+
+template <class C>
+__device__ __forceinline__ f16x8 read_nc(const char LDS_AS* bs, int n, int c, int lane) {
+  // ds_read_b64_tr_b16 on a 16-lane group: lane t supplies the address of the
+  // 4 halves B[k0 + t/4][n + 4(t%4) ...]; it receives B[k0 + e][n + t], e < 4.
+  // The two 4-half results are joined as whole vectors: extracting their
+  // elements one by one is miscompiled by this hipcc (every element became
+  // element 0), and the whole-vector form needs no extra VALU moves.
+  const int t = lane & 15, g = lane >> 4;
+  i16x4 v[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int krow = kChunk * c + 8 * g + 4 * h + (t >> 2);
+    const int nn = n + 4 * (t & 3);
+    const int u = (nn >> 3) ^ (nc_swz(krow) & (C::UB - 1));
+    const char LDS_AS* addr = bs + krow * (C::BN * 2) + (u << 4) + ((nn & 7) << 1);
+    v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((i16x4 LDS_AS*)addr);
+  }
+  typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+  return __builtin_shufflevector(__builtin_bit_cast(f16x4, v[0]), __builtin_bit_cast(f16x4, v[1]), 0, 1, 2, 3, 4,
+                                 5, 6, 7);
+}
+
+template <class C, bool CHUNKED>
+__device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, int wn, int lane,
+                                              f32x4 (&acc)[C::FM][C::FN]) {
+  const char LDS_AS* as = stage;
+  const char LDS_AS* bs = stage + C::A_STAGE;
+  const int r16 = lane & 15, g = lane >> 4;
+  f16x8 af[C::FM][2];
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) af[i][c] = read_kc<C>(as, wm * C::WTM + 16 * i + r16, 4 * c + g);
+  const f16x2 ones = {(f16)1.0f, (f16)1.0f};
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < C::FN; ++j) {
+    f16x8 bf[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      if (C::BL == kKC)
+        bf[c] = read_kc<C>(bs, wn * C::WTN + 16 * j + r16, 4 * c + g);
+      else
+        bf[c] = read_nc<C>(bs, wn * C::WTN + 16 * j, c, lane);
+    }
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i) {
+      // operands swapped (b first) so lane l receives C[row l%16][4 consecutive columns]
+      if (CHUNKED) {
+        const f32x4 p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[0], af[i][0], zero, 0, 0, 0);
+        const f32x4 p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[1], af[i][1], zero, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const f32x2 pr = {p0[r], p1[r]};
+          const f16x2 h = __builtin_convertvector(pr, f16x2);  // v_cvt_pk_f16_f32, RNE
+          acc[i][j][r] = __builtin_amdgcn_fdot2(h, ones, acc[i][j][r], false);
+        }
+      } else {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[0], af[i][0], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[1], af[i][1], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// Whole K loop of the fast path: two LDS stages, the copy of stage s+1 in
+// flight while stage s is multiplied.
+template <class C, bool CHUNKED>
+__device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t n0, char LDS_AS* smem,
+                                            FastLoader<C>& ld, int tid, int wave, int wm, int wn, int lane,
+                                            f32x4 (&acc)[C::FM][C::FN]) {
+  const int64_t nsteps = (p.K + kStageK - 1) / kStageK;
+  if (nsteps == 0) return;
+  ld.issue(p, m0, n0, 0, smem, wave);
+  for (int64_t s = 0; s < nsteps; ++s) {
+    wait_vm0();
+    __syncthreads();
+    char LDS_AS* cur = smem + (s & 1) * C::STAGE;
+    if (s + 1 < nsteps) ld.issue(p, m0, n0, (s + 1) * kStageK, smem + ((s + 1) & 1) * C::STAGE, wave);
+    compute_stage<C, CHUNKED>(cur, wm, wn, lane, acc);
+  }
+  __syncthreads();  // LDS free for a redo pass
+}
+
+// Generic path: gathers elements with any strides through registers into
+// the KC layout (both operands), one stage at a time.
+template <class C>
+__device__ __forceinline__ void stage_generic(const Params& p, int64_t m0, int64_t n0, int64_t kbase,
+                                              char LDS_AS* stage, int tid) {
+#pragma unroll
+  for (int j = 0; j < C::LA; ++j) {
+    const int s = j * C::T + tid, row = s >> 3, u = (s & 7) ^ kc_swz(row);
+    const int64_t m = m0 + row;
+    f16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t k = kbase + 8 * u + e;
+      v[e] = (m < p.M && k < p.K) ? p.a[m * p.sam + k * p.sak] : (f16)0.0f;
+    }
+    *(f16x8 LDS_AS*)(stage + s * 16) = v;
+  }
+#pragma unroll
+  for (int j = 0; j < C::LB; ++j) {
+    const int s = j * C::T + tid, row = s >> 3, u = (s & 7) ^ kc_swz(row);
+    const int64_t n = n0 + row;
+    f16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t k = kbase + 8 * u + e;
+      v[e] = (n < p.N && k < p.K) ? p.b[k * p.sbk + n * p.sbn] : (f16)0.0f;
+    }
+    *(f16x8 LDS_AS*)(stage + C::A_STAGE + s * 16) = v;
+  }
+}
+
+template <class C, bool CHUNKED>
+__device__ __forceinline__ void k_loop_generic(const Params& p, int64_t m0, int64_t n0, char LDS_AS* smem,
+                                               int tid, int wm, int wn, int lane, f32x4 (&acc)[C::FM][C::FN]) {
+  const int64_t nsteps = (p.K + kStageK - 1) / kStageK;
+  for (int64_t s = 0; s < nsteps; ++s) {
+    stage_generic<C>(p, m0, n0, s * kStageK, smem, tid);
+    __syncthreads();
+    compute_stage<C, CHUNKED>(smem, wm, wn, lane, acc);
+    __syncthreads();
+  }
+}
+
+template <class C, bool OUT32>
+__device__ __forceinline__ void store_tile(const Params& p, int64_t m0, int64_t n0, int wm, int wn, int lane,
+                                           const f32x4 (&acc)[C::FM][C::FN]) {
+  const int r16 = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i) {
+    const int64_t row = m0 + wm * C::WTM + 16 * i + r16;
+    if (row >= p.M) continue;
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) {
+      const int64_t col = n0 + wn * C::WTN + 16 * j + 4 * g;
+      const f32x4 v = acc[i][j];
+      if (p.vec_store && col + 3 < p.N) {
+        if (OUT32) {
+          *(f32x4*)((float*)p.c + row * p.scm + col) = v;
+        } else {
+          const f32x2 lo = {v[0], v[1]}, hi = {v[2], v[3]};
+          const f16x2 hl = __builtin_convertvector(lo, f16x2), hh = __builtin_convertvector(hi, f16x2);
+          typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+          const f16x4 o = {hl[0], hl[1], hh[0], hh[1]};
+          *(f16x4*)((f16*)p.c + row * p.scm + col) = o;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (col + r >= p.N) break;
+          const int64_t off = row * p.scm + (col + r) * p.scn;
+          if (OUT32)
+            ((float*)p.c)[off] = v[r];
+          else
+            ((f16*)p.c)[off] = (f16)v[r];
+        }
+      }
+    }
+  }
+}
+
+// One kernel body for both families: FAST selects the direct-to-LDS loader.
+template <class C, bool FAST, bool CHUNKED, bool OUT32>
+__global__ __launch_bounds__(C::T) void gemm_kernel(Params p) {
+  __shared__ __attribute__((aligned(1024))) char smem_raw[FAST ? 2 * C::STAGE : C::STAGE];
+  __shared__ int tile_bad;
+  char LDS_AS* smem = (char LDS_AS*)smem_raw;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+  int64_t tm, tn;
+  block_tile(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
+  const int64_t m0 = tm * C::BM, n0 = tn * C::BN;
+
+  if (CHUNKED && tid == 0) tile_bad = 0;
+
+  f32x4 acc[C::FM][C::FN];
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  FastLoader<C> ld;
+  if (FAST) {
+    ld.init(p, m0, n0, tid);
+    k_loop_fast<C, CHUNKED>(p, m0, n0, smem, ld, tid, wave, wm, wn, lane, acc);
+  } else {
+    k_loop_generic<C, CHUNKED>(p, m0, n0, smem, tid, wm, wn, lane, acc);
+  }
+
+  if (CHUNKED) {
+    // tile flag: any element of the FP32 sum inf or NaN (kernel.py:70-71)
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bad |= !(__builtin_fabsf(acc[i][j][r]) < __builtin_inff());
+    if (bad) tile_bad = 1;
+    __syncthreads();
+    const int flag = tile_bad;
+    if (p.flags && tid == 0) p.flags[tm * p.tiles_n + tn] = (uint8_t)flag;
+    if (flag) {
+      // redo the whole tile with FP32 accumulation (kernel.py:75-81)
+#pragma unroll
+      for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (FAST)
+        k_loop_fast<C, false>(p, m0, n0, smem, ld, tid, wave, wm, wn, lane, acc);
+      else
+        k_loop_generic<C, false>(p, m0, n0, smem, tid, wm, wn, lane, acc);
+    }
+  }
+  store_tile<C, OUT32>(p, m0, n0, wm, wn, lane, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Host side: per-shape tile table and launch.
+// ---------------------------------------------------------------------------
+using CfgL_KC = Cfg<256, 256, 4, 2, kKC>;  // 8 waves, 64x128 per wave, 128 KiB LDS
+using CfgL_NC = Cfg<256, 256, 4, 2, kNC>;
+using CfgM_KC = Cfg<128, 128, 2, 2, kKC>;  // 4 waves, 64x64 per wave, 64 KiB LDS
+using CfgM_NC = Cfg<128, 128, 2, 2, kNC>;
+using CfgG = Cfg<128, 128, 2, 2, kKC>;     // generic gather path (single LDS stage)
+
+enum Family { kFast = 0, kGeneric = 1 };
+
+struct Choice {
+  int bm, bn, family, threads, blayout;
+};
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline int cu_count() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+  return n;
+}
+
+// Which loader the operands allow.  blayout: kKC / kNC, or -1 for generic.
+inline int fast_layout(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                       const void* a, const void* b, int bm, int bn) {
+  const bool a_ok = (sak == 1 || K <= 1) && sam % 8 == 0 && ((uintptr_t)a % 16) == 0 && K % 8 == 0 &&
+                    (int64_t)bm * sam * 2 + 4 * kStageK < kOob;
+  if (!a_ok) return -1;
+  const bool b_kc = (sbk == 1 || K <= 1) && sbn % 8 == 0 && ((uintptr_t)b % 16) == 0 && K % 8 == 0 &&
+                    (int64_t)bn * sbn * 2 + 4 * kStageK < kOob;
+  if (b_kc) return kKC;
+  const bool b_nc = (sbn == 1 || N <= 1) && sbk % 8 == 0 && ((uintptr_t)b % 16) == 0 && N % 8 == 0 &&
+                    (int64_t)kStageK * sbk * 2 + 2 * bn < kOob;
+  if (b_nc) return kNC;
+  return -1;
+  (void)M;
+}
+
+inline Choice choose(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                     const void* a, const void* b) {
+  // Big tiles when they alone fill every CU; otherwise 128x128 (4x the tiles).
+  const int cus = cu_count();
+  const bool big = cdiv(M, 256) * cdiv(N, 256) >= cus;
+  const int bm = big ? 256 : 128, bn = bm;
+  const int bl = fast_layout(M, N, K, sam, sak, sbk, sbn, a, b, bm, bn);
+  if (bl < 0) return Choice{CfgG::BM, CfgG::BN, kGeneric, CfgG::T, kKC};
+  return Choice{bm, bn, kFast, big ? CfgL_KC::T : CfgM_KC::T, bl};
+}
+
+template <class C, bool FAST>
+hipError_t launch_cfg(const Params& p, int out32, int chunked, hipStream_t st) {
+  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(C::T);
+  if (chunked) {
+    if (out32)
+      hipLaunchKernelGGL((gemm_kernel<C, FAST, true, true>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((gemm_kernel<C, FAST, true, false>), grid, block, 0, st, p);
+  } else {
+    if (out32)
+      hipLaunchKernelGGL((gemm_kernel<C, FAST, false, true>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((gemm_kernel<C, FAST, false, false>), grid, block, 0, st, p);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" {
+
+int f16acc_abi_version(void) { return 1; }
+
+const char* f16acc_strerror(int code) {
+  if (code == 0) return "success";
+  if (code == F16ACC_E_ARG) return "f16acc: invalid argument";
+  if (code == F16ACC_E_UNSUPPORTED) return "f16acc: unsupported layout or extent";
+  if (code > 0) return hipGetErrorString((hipError_t)code);
+  return "f16acc: unknown error";
+}
+
+int f16acc_block_tile(int64_t block, int64_t tiles_m, int64_t tiles_n, int64_t* tile_m, int64_t* tile_n) {
+  if (tiles_m <= 0 || tiles_n <= 0 || block < 0 || block >= tiles_m * tiles_n || !tile_m || !tile_n)
+    return F16ACC_E_ARG;
+  block_tile(block, tiles_m, tiles_n, tile_m, tile_n);
+  return 0;
+}
+
+int f16acc_tile_config(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                       const void* a, const void* b, int* bm, int* bn, int64_t* tiles_m, int64_t* tiles_n,
+                       int* family, int* threads) {
+  if (M < 0 || N < 0 || K < 0) return F16ACC_E_ARG;
+  const Choice ch = choose(M, N, K, sam, sak, sbk, sbn, a, b);
+  if (bm) *bm = ch.bm;
+  if (bn) *bn = ch.bn;
+  if (tiles_m) *tiles_m = cdiv(M, ch.bm);
+  if (tiles_n) *tiles_n = cdiv(N, ch.bn);
+  if (family) *family = ch.family;
+  if (threads) *threads = ch.threads;
+  return 0;
+}
+
+int f16acc_gemm(const void* a, const void* b, void* c, uint8_t* tile_flags, int64_t M, int64_t N, int64_t K,
+                int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int out_dtype,
+                int chunked, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return F16ACC_E_ARG;
+  if (out_dtype != F16ACC_OUT_F16 && out_dtype != F16ACC_OUT_F32) return F16ACC_E_ARG;
+  if (chunked != 0 && chunked != 1) return F16ACC_E_ARG;
+  if (M == 0 || N == 0) return 0;  // nothing to write (Triton skips an empty grid too)
+  if (!c || (K > 0 && (!a || !b))) return F16ACC_E_ARG;
+  const Choice ch = choose(M, N, K, sam, sak, sbk, sbn, a, b);
+  Params p;
+  p.a = (const f16*)a;
+  p.b = (const f16*)b;
+  p.c = c;
+  p.flags = tile_flags;
+  p.M = M; p.N = N; p.K = K;
+  p.sam = sam; p.sak = sak; p.sbk = sbk; p.sbn = sbn; p.scm = scm; p.scn = scn;
+  p.tiles_m = cdiv(M, ch.bm);
+  p.tiles_n = cdiv(N, ch.bn);
+  const int esize = out_dtype == F16ACC_OUT_F32 ? 4 : 2;
+  p.vec_store = scn == 1 && (scm * esize) % 16 == 0 && ((uintptr_t)c % 16) == 0;
+  if (p.tiles_m * p.tiles_n > 0x7fffffff) return F16ACC_E_UNSUPPORTED;
+  const int out32 = out_dtype == F16ACC_OUT_F32;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (ch.family == kGeneric)
+    e = launch_cfg<CfgG, false>(p, out32, chunked, st);
+  else if (ch.bm == 256)
+    e = ch.blayout == kKC ? launch_cfg<CfgL_KC, true>(p, out32, chunked, st)
+                          : launch_cfg<CfgL_NC, true>(p, out32, chunked, st);
+  else
+    e = ch.blayout == kKC ? launch_cfg<CfgM_KC, true>(p, out32, chunked, st)
+                          : launch_cfg<CfgM_NC, true>(p, out32, chunked, st);
+  return (int)e;
+}
+
+}  // extern "C"

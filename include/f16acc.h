@@ -1,0 +1,98 @@
+/*
+ * f16acc for MI355X (gfx950): C ABI of the chunked FP16 GEMM.
+ *
+ * Plain C types only (pointers, 64-bit sizes and strides in elements), so any
+ * host language can bind it; the Python package binds it through ctypes.
+ * Every entry point is reentrant: the library keeps no per-call state.
+ *
+ * Return codes: 0 on success, a positive hipError_t value when the HIP
+ * runtime failed, or one of the negative F16ACC_E_* codes below for
+ * arguments the library rejects before launching anything.
+ */
+#ifndef F16ACC_H
+#define F16ACC_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define F16ACC_OUT_F16 0
+#define F16ACC_OUT_F32 1
+
+#define F16ACC_E_ARG (-1)        /* negative size, null pointer with work to do, bad enum */
+#define F16ACC_E_UNSUPPORTED (-2) /* a layout / extent this build cannot address */
+
+/*
+ * c[M,N] = a[M,K] @ b[K,N]; a and b binary16, c binary16 or binary32.
+ *
+ * Replaces the reference's host op and its two Triton launches,
+ * f16acc/kernel.py:84-105 (mm -> _gemm[grid] at :99 and _redo[grid] at
+ * :103-104).  Shape / dtype / device validation stays in the Python layer
+ * (kernel.py:87-90 raise ValueError there); this function re-checks only what
+ * it needs to stay in bounds.
+ *
+ *   a, b, c           device pointers (HIP), element strides may be anything,
+ *                     including the stride-(1, K) view w.t() of an nn.Linear
+ *                     weight (kernel.py:84, patch.py:28)
+ *   tile_flags        optional (may be NULL): receives one byte per output
+ *                     tile, row-major over the tile grid of f16acc_tile_config,
+ *                     1 where the tile's chunked FP32 sum held inf or NaN and
+ *                     was recomputed with FP32 accumulation (kernel.py:70-71,
+ *                     75-81); sized f16acc_tile_config's tiles_m * tiles_n
+ *   M, N, K           sizes; M == 0 or N == 0 launches nothing, K == 0 writes 0
+ *   sam, sak          a strides (elements): a[i][k] = a[i*sam + k*sak]
+ *   sbk, sbn          b strides: b[k][j] = b[k*sbk + j*sbn]
+ *   scm, scn          c strides
+ *   out_dtype         F16ACC_OUT_F16 or F16ACC_OUT_F32 (kernel.py:93 c dtype)
+ *   chunked           1: 32-long K chunks rounded to binary16 and added into
+ *                     an FP32 sum, non-finite tiles redone in FP32 on the same
+ *                     stream without a host sync (kernel.py:49, 70-81);
+ *                     0: plain FP32 accumulation (kernel.py:50-51)
+ *   stream            hipStream_t to launch on (NULL = the null stream)
+ *
+ * All offsets are 64-bit, so outputs past 2^31 elements are addressed
+ * correctly (kernel.py:97-98 switches Triton to int64 for that).
+ */
+int f16acc_gemm(const void* a, const void* b, void* c, uint8_t* tile_flags,
+                int64_t M, int64_t N, int64_t K,
+                int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                int64_t scm, int64_t scn,
+                int out_dtype, int chunked, void* stream);
+
+/*
+ * The tile configuration f16acc_gemm picks for a problem: replaces the
+ * reference's autotuned CONFIGS table and best_config handoff
+ * (f16acc/kernel.py:16-19, 63, 101-102) with a fixed per-shape table.
+ * Writes the workgroup tile (bm x bn), the tile grid, the kernel family
+ * (0 = direct-to-LDS fast path, 1 = generic strided path) and the number of
+ * threads per workgroup.  Any output pointer may be NULL.
+ */
+int f16acc_tile_config(int64_t M, int64_t N, int64_t K,
+                       int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                       const void* a, const void* b,
+                       int* bm, int* bn, int64_t* tiles_m, int64_t* tiles_n,
+                       int* family, int* threads);
+
+/*
+ * Output tile processed by workgroup `block` of a launch over a
+ * tiles_m x tiles_n grid (the XCD-aware, group-M swizzled order the kernels
+ * use).  Exposed so the mapping can be checked on the host; the reference's
+ * counterpart is _tile, f16acc/kernel.py:22-34.  Returns F16ACC_E_ARG when
+ * block is outside [0, tiles_m * tiles_n).
+ */
+int f16acc_block_tile(int64_t block, int64_t tiles_m, int64_t tiles_n,
+                      int64_t* tile_m, int64_t* tile_n);
+
+/* Short text for a return code of this library (never NULL). */
+const char* f16acc_strerror(int code);
+
+/* ABI version: bumped whenever a signature above changes. */
+int f16acc_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* F16ACC_H */
