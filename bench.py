@@ -1,0 +1,217 @@
+"""Benchmark of the chunked FP16 GEMM on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+
+A step is one f16acc_amd.mm call on inputs already resident in HBM.  The
+default workload is the headline one: M = N = K = 4096, A and B ~ N(0, 1)
+cast to fp16, B row-major [K, N] (as the reference's bench/gemm_bench.py
+passes it), fp16 output, chunk-32 with FP32 chunk sum and in-kernel overflow
+redo.  Prints one JSON line:
+  value       TFLOPS of the timed steps (2 M N K per step)
+  roofline    the GEMM kernel's achieved TFLOP/s (HIP events over the timed
+              region on the launch stream) against the MI355X dense fp16
+              MFMA peak; traffic = HBM bytes per launch from the rocprofv3
+              FETCH_SIZE / WRITE_SIZE summary in profiles/, when present
+  cpu_baseline the reference algorithm (the CPU oracle) on this host's cores
+  hipblaslt   torch.mm (hipBLASLt) on the same inputs and GPU
+  max_rel_err_vs_fp64 / max_rel_err_vs_oracle  the reference's error metric
+Other workloads (--workload) are sweeps for the design record, not bench lines.
+"""
+
+import argparse
+import json
+import os
+import re
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_TFLOPS = 2516.6  # MI355X dense fp16 MFMA: 256 CU x 2.4 GHz x 4096 flop/clk
+METRIC = "TFLOPS at 4096³ fp16 GEMM (1 GPU, % of fp16 MFMA peak); max rel err vs FP64"
+REF_TFLOPS = 65.7  # reference README.md:29, RTX 4060 Ti, same GEMM (fp16 out)
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_4096_fp16out_rowmajorB_traffic.txt")
+
+WORKLOADS = {
+    # name: (M, N, K, b_layout, out_dtype)
+    "gemm4096": (4096, 4096, 4096, "row", torch.float16),
+    "gemm4096_bt": (4096, 4096, 4096, "t", torch.float16),
+    "gemm4096_f32": (4096, 4096, 4096, "row", torch.float32),
+    "gemm8192": (8192, 8192, 8192, "row", torch.float16),
+    "gemm8192_bt": (8192, 8192, 8192, "t", torch.float16),
+    "qwen_qo": (2048, 1536, 1536, "t", torch.float16),
+    "qwen_kv": (2048, 256, 1536, "t", torch.float16),
+    "qwen_gateup": (2048, 8960, 1536, "t", torch.float16),
+    "qwen_down": (2048, 1536, 8960, "t", torch.float16),
+    "odd": (2049, 1537, 8961, "t", torch.float16),
+}
+
+
+def make_inputs(M, N, K, layout, seed=0, device="cuda"):
+    """Seeded CPU inputs (the oracle sees the same bits), copied to the GPU.
+    layout "row": b is [K, N] row-major; "t": b is the w.t() view of [N, K]."""
+    g = torch.Generator().manual_seed(seed)
+    a = torch.randn(M, K, generator=g).half()
+    if layout == "row":
+        b = torch.randn(K, N, generator=g).half()
+        gb = b.to(device)
+    else:
+        w = torch.randn(N, K, generator=g).half()
+        b = w.t()
+        gb = w.to(device).t()
+    return a, b, a.to(device), gb
+
+
+def time_steps(op, steps, warmup):
+    """Warm up, then time exactly `steps` calls between two synchronisations.
+    Returns (total seconds, event seconds on the current stream)."""
+    for _ in range(warmup):
+        op()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        op()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall, start.elapsed_time(stop) / 1e3
+
+
+def median_event_time(op, iters=30, warmup=10):
+    for _ in range(warmup):
+        op()
+    torch.cuda.synchronize()
+    vals = []
+    for _ in range(iters):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        op()
+        e.record()
+        torch.cuda.synchronize()
+        vals.append(s.elapsed_time(e) / 1e3)
+    return statistics.median(vals)
+
+
+def read_traffic():
+    """HBM bytes per launch from the committed rocprofv3 counter summary."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read(), re.M)
+        return float(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
+def cpu_baseline(a, b, out_dtype, budget_s=20.0):
+    """The reference algorithm (oracle.chunk32, PyTorch on the CPU) on this
+    host's cores, on the same inputs; repeated while within budget."""
+    from oracle import chunk32
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    M, K = a.shape
+    N = b.shape[1]
+    times, ref = [], None
+    t_start = time.perf_counter()
+    while not times or (time.perf_counter() - t_start + times[-1] < budget_s and len(times) < 3):
+        t0 = time.perf_counter()
+        ref = chunk32.mm(a, b, out_dtype)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    info = {"value": 2.0 * M * N * K / t / 1e12, "unit": "TFLOPS", "cores": threads, "kind": "port",
+            "sample": f"the full {M}x{N}x{K} GEMM (oracle/chunk32.py, torch CPU, {threads} threads), "
+                      f"median of {len(times)} run(s), {t:.2f} s each"}
+    return info, ref
+
+
+def copy_reference(steps, warmup, nbytes=1 << 30):
+    """A plain device copy of known size (1 GiB read + 1 GiB written per step):
+    the calibration for rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
+    src = torch.ones(nbytes // 2, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    wall, ev = time_steps(lambda: dst.copy_(src), steps, warmup)
+    print(json.dumps({"workload": "copy", "bytes_read_per_step": nbytes, "bytes_written_per_step": nbytes,
+                      "GB_per_s": round(2 * nbytes * steps / ev / 1e9, 1), "steps": steps}), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="gemm4096", choices=sorted(WORKLOADS) + ["copy"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and oracle comparison")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (a GEMM shards by M or N "
+              "tiles with no exchange, see DESIGN.md); run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    if args.workload == "copy":
+        return copy_reference(args.steps, args.warmup)
+
+    import f16acc_amd
+    from f16acc_amd.kernel import tile_config
+
+    torch.backends.cuda.matmul.allow_fp16_reduced_precision_reduction = False
+    M, N, K, layout, out_dtype = WORKLOADS[args.workload]
+    a_cpu, b_cpu, a, b = make_inputs(M, N, K, layout)
+    flops = 2.0 * M * N * K
+    cfg = tile_config(a, b)
+
+    op = lambda: f16acc_amd.mm(a, b, out_dtype)  # noqa: E731
+    wall, ev = time_steps(op, args.steps, args.warmup)
+    value = flops * args.steps / wall / 1e12
+    kernel_s = ev / args.steps  # average per launch, HIP events on the launch stream
+    achieved = flops / kernel_s / 1e12
+
+    c = op()
+    torch.cuda.synchronize()
+    ref64 = a.double() @ b.double()
+    err_fp64 = ((c.double() - ref64).abs().max() / ref64.abs().max()).item()
+    del ref64
+
+    blas_t = median_event_time(lambda: torch.mm(a, b) if out_dtype == torch.float16 else torch.mm(a, b).float())
+    fp32acc_t = median_event_time(lambda: f16acc_amd.mm(a, b, out_dtype, chunked=False))
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": round(value / REF_TFLOPS, 2) if args.workload == "gemm4096" else None,
+        "baseline_note": "vs_baseline divides by the reference's 65.7 TFLOPS on an RTX 4060 Ti (README.md:29)",
+        "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": f"fp16 GEMM M={M} N={N} K={K}, A,B~N(0,1) seeded, B "
+                               f"{'row-major [K,N]' if layout == 'row' else 'w.t() of [N,K]'}, "
+                               f"{'fp16' if out_dtype == torch.float16 else 'fp32'} out, chunk-32 + FP32 sum "
+                               f"+ in-kernel overflow redo", "name": args.workload,
+                   "tile": f"{cfg['bm']}x{cfg['bn']}", "tiles": cfg["tiles_m"] * cfg["tiles_n"],
+                   "kernel_family": cfg["family"]},
+        "frac_of_peak": round(value / PEAK_TFLOPS, 4),
+        "max_rel_err_vs_fp64": err_fp64,
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": read_traffic(),
+                     "kernel_us": round(kernel_s * 1e6, 2)},
+        "hipblaslt": {"value": round(flops / blas_t / 1e12, 2), "unit": "TFLOPS",
+                      "op": "torch.mm (hipBLASLt), same inputs", "us": round(blas_t * 1e6, 2)},
+        "fp32_accumulate": {"value": round(flops / fp32acc_t / 1e12, 2), "unit": "TFLOPS",
+                            "op": "f16acc_amd.mm(chunked=False)", "us": round(fp32acc_t * 1e6, 2)},
+    }
+    if not args.no_cpu:
+        info, ref = cpu_baseline(a_cpu, b_cpu, out_dtype)
+        line["cpu_baseline"] = info
+        from oracle.chunk32 import rel
+
+        line["max_rel_err_vs_oracle"] = rel(c.cpu(), ref)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
