@@ -112,3 +112,16 @@ def rel(x, ref):
     x, ref = x.double(), ref.double()
     den = ref.abs().max()
     return ((x - ref).abs().max() / den).item() if den > 0 else (x - ref).abs().max().item()
+
+
+def rel_finite(x, ref):
+    """rel over the elements finite in ref, after checking that the others
+    match exactly (inf with the same sign, NaN where ref is NaN); returns inf
+    when they do not."""
+    x, ref = x.double().cpu(), ref.double().cpu()
+    fin = torch.isfinite(ref)
+    same_nonfinite = torch.equal(torch.isnan(x), torch.isnan(ref)) and torch.equal(
+        x[torch.isinf(ref)], ref[torch.isinf(ref)])
+    if not same_nonfinite or not torch.isfinite(x[fin]).all():
+        return float("inf")
+    return rel(x[fin], ref[fin]) if fin.any() else 0.0

@@ -1,0 +1,145 @@
+"""The drop-in boundary without a GPU: the C ABI library loads and exports
+every symbol include/f16acc.h declares, rejects bad arguments before any
+launch, maps blocks to tiles bijectively, and the Python surface raises the
+reference's errors and routes calls the reference's way
+(f16acc/kernel.py:84-90, f16acc/patch.py:17-40 of the reference).
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import f16acc_amd as f16acc
+from f16acc_amd import _lib, patch
+from f16acc_amd.kernel import tile_config
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    src = open(os.path.join(ROOT, "include", "f16acc.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(f16acc_\w+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = header_functions()
+    assert names, "no declarations parsed"
+    dll = ctypes.CDLL(_lib.LIB)
+    for name in names:
+        assert hasattr(dll, name), name
+    assert sorted(_lib.EXPORTS) == names
+    assert _lib.abi_version() == 1
+
+
+def test_gemm_rejects_bad_arguments_before_launching():
+    args = dict(M=16, N=16, K=16, sam=16, sak=1, sbk=16, sbn=1, scm=16, scn=1)
+
+    def call(ptrs=(8, 8, 8), out=0, chunked=1, **kw):
+        a = {**args, **kw}
+        return _lib.gemm(ptrs[0], ptrs[1], ptrs[2], None, a["M"], a["N"], a["K"], a["sam"], a["sak"], a["sbk"],
+                         a["sbn"], a["scm"], a["scn"], out, chunked, None)
+
+    assert call(M=-1) == _lib.E_ARG
+    assert call(K=-5) == _lib.E_ARG
+    assert call(out=2) == _lib.E_ARG
+    assert call(chunked=7) == _lib.E_ARG
+    assert call(ptrs=(0, 8, 8)) == _lib.E_ARG  # null a with K > 0
+    assert call(ptrs=(8, 8, 0)) == _lib.E_ARG  # null c
+    assert call(M=0) == 0 and call(N=0) == 0  # empty output: nothing launched
+    assert _lib.strerror(_lib.E_ARG).decode().startswith("f16acc")
+
+
+def test_block_to_tile_map_is_a_bijection():
+    """Brute force over grids, including ones not divisible by the 8 XCDs or
+    the group width (the reference's _tile, kernel.py:22-34, covers every tile
+    once; so must the XCD-aware map)."""
+    tm, tn = ctypes.c_int64(), ctypes.c_int64()
+    for gm in list(range(1, 18)) + [32, 33, 63]:
+        for gn in list(range(1, 18)) + [35, 70]:
+            seen = set()
+            for b in range(gm * gn):
+                assert _lib.block_tile(b, gm, gn, ctypes.byref(tm), ctypes.byref(tn)) == 0
+                assert 0 <= tm.value < gm and 0 <= tn.value < gn
+                seen.add((tm.value, tn.value))
+            assert len(seen) == gm * gn
+    assert _lib.block_tile(6, 2, 3, ctypes.byref(tm), ctypes.byref(tn)) == _lib.E_ARG
+
+
+def test_block_map_keeps_each_xcd_on_a_compact_patch():
+    """4096^2 with 256 x 256 tiles: 16 x 16 tiles, 32 per XCD; each XCD's
+    tiles should touch few A row-blocks and B column-blocks."""
+    tm, tn = ctypes.c_int64(), ctypes.c_int64()
+    for xcd in range(8):
+        rows, cols = set(), set()
+        for b in range(xcd, 256, 8):
+            _lib.block_tile(b, 16, 16, ctypes.byref(tm), ctypes.byref(tn))
+            rows.add(tm.value)
+            cols.add(tn.value)
+        assert len(rows) * len(cols) == 32
+
+
+class _Fake:
+    """Stands in for a tensor in tile_config (shape, strides, data_ptr)."""
+
+    def __init__(self, shape, strides, ptr=4096):
+        self.shape, self._strides, self._ptr = shape, strides, ptr
+
+    def stride(self, i):
+        return self._strides[i]
+
+    def data_ptr(self):
+        return self._ptr
+
+
+@pytest.mark.parametrize("M,N,K,sa,sb,fam,bm", [
+    (4096, 4096, 4096, (4096, 1), (4096, 1), "fast", 256),   # row-major b (NC loader)
+    (4096, 4096, 4096, (4096, 1), (1, 4096), "fast", 256),   # w.t() (KC loader)
+    (2048, 1536, 1536, (1536, 1), (1, 1536), "fast", 128),   # too few 256-tiles to fill the CUs
+    (2049, 1537, 8961, (8961, 1), (1, 8961), "generic", 128),  # rows not 16-byte aligned
+    (300, 200, 256, (512, 2), (700, 3), "generic", 128),      # strided operands
+])
+def test_tile_table(M, N, K, sa, sb, fam, bm):
+    cfg = tile_config(_Fake((M, K), sa), _Fake((K, N), sb))
+    assert cfg["family"] == fam and cfg["bm"] == bm
+    assert cfg["tiles_m"] == -(-M // cfg["bm"]) and cfg["tiles_n"] == -(-N // cfg["bn"])
+
+
+def test_misaligned_pointer_takes_the_generic_path():
+    cfg = tile_config(_Fake((4096, 4096), (4096, 1), ptr=4098), _Fake((4096, 4096), (4096, 1)))
+    assert cfg["family"] == "generic"
+
+
+def test_bad_inputs_raise_value_error():
+    # reference tests/test_f16acc.py:42-47 (runs here on CPU tensors: the device
+    # check fires first for CPU operands, the shape check for mismatched K)
+    a = torch.randn(256, 64).half()
+    for bad in (torch.randn(32, 64).half(), torch.randn(64, 64), torch.randn(64, 64).half()):
+        with pytest.raises(ValueError):
+            f16acc.mm(a, bad)
+    with pytest.raises(ValueError):
+        f16acc.mm(a, torch.randn(64, 8).half(), out_dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        f16acc.mm(torch.randn(4, 4, 4).half(), torch.randn(4, 4).half())
+
+
+def test_patch_enable_disable_and_cpu_fallback():
+    for k in patch.calls:
+        patch.calls[k] = 0
+    lin = torch.nn.Linear(64, 32).half()
+    f16acc.enable()
+    try:
+        assert torch.nn.functional.linear is patch.linear
+        with torch.no_grad():
+            y = lin(torch.randn(256, 64).half())  # CPU input: stays on the original
+        assert y.shape == (256, 32)
+        assert patch.calls == {"chunked": 0, "original": 1}
+    finally:
+        f16acc.disable()
+    assert torch.nn.functional.linear is patch._orig
+    assert patch.MIN_ROWS == 128
+    assert f16acc.calls is patch.calls
+    assert set(f16acc.__all__) == {"mm", "enable", "disable", "calls"}
