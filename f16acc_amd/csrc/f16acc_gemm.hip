@@ -8,15 +8,21 @@
 // FP32 accumulation by the same workgroup, so there is no second launch and
 // no host sync.
 //
-// gfx950 has no FP16-accumulating MFMA, so the chunk is one
+// gfx950 has no FP16-accumulating MFMA, so a chunk is one
 // v_mfma_f32_16x16x32_f16 with a zero accumulator (K = 32 = one chunk), and
-// the rounding is done in the epilogue of each MFMA pair:
-//   v_cvt_pk_f16_f32  packs the partials of two consecutive chunks of the
-//                     same element into one register (RNE, inf past 65504)
-//   v_dot2_f32_f16    adds both halves into the FP32 sum (x*1 + y*1 + s)
-// i.e. one VALU instruction per output element per chunk next to 64 MFMA
-// flops, which a 16x16x32 MFMA (16 cycles for 256 elements) and the VALU
-// (4 cycles per wave64 instruction) can overlap.
+// the chunk semantics are emulated per pair of chunks of a 16x16 block:
+//   v_cvt_pk_f16_f32  rounds the FP32 partials of two consecutive chunks of
+//                     the same element into one register (RNE, inf past 65504)
+//   selector MFMA     one more v_mfma_f32_16x16x32_f16 against a constant 0/1
+//                     matrix adds both FP16 halves into the FP32 sum (exact
+//                     products, see chunk_pair_selector)
+// so a chunk pair costs three MFMAs and four VALU conversions.  Measured on
+// MI355X, VALU work and MFMAs overlap only partly and v_dot2_f32_f16 stalls
+// the matrix pipe outright, so summing on the MFMA pipe is the faster form:
+// 3 MFMAs + 4 v_cvt_pk per block step run at ~0.63 of the plain FP32-
+// accumulating MFMA rate (ceiling 2/3), against ~0.46 for cvt + v_dot2.
+// The steps are software pipelined (see compute_stage) so no instruction
+// waits on the MFMA that produces its operand.
 //
 // Data path per workgroup: operand tiles are staged global -> LDS with
 // buffer_load_dwordx4 ... lds (no VGPR round trip), 64 K (two chunks) per
@@ -49,7 +55,7 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 #define LDS_AS __attribute__((address_space(3)))
 
 constexpr int kChunk = 32;      // reference BLOCK_K (kernel.py:17): the rounding interval
-constexpr int kStageK = 64;     // K per LDS stage: two chunks, paired by v_dot2
+constexpr int kStageK = 64;     // K per LDS stage: one chunk pair
 constexpr int kNumXcd = 8;      // MI355X: workgroups are dealt round-robin over 8 XCDs
 constexpr int kGroupM = 8;      // group-M swizzle width (reference G = 8, kernel.py:17)
 constexpr int kOob = 0x7fffff00;  // buffer offset past num_records: the load returns 0
@@ -230,6 +236,45 @@ __device__ __forceinline__ f16x8 read_nc(const char LDS_AS* bs, int n, int c, in
                                  5, 6, 7);
 }
 
+template <class C>
+__device__ __forceinline__ f16x8 read_b(const char LDS_AS* bs, int wn, int j, int c, int lane) {
+  if (C::BL == kKC) return read_kc<C>(bs, wn * C::WTN + 16 * j + (lane & 15), 4 * c + (lane >> 4));
+  return read_nc<C>(bs, wn * C::WTN + 16 * j, c, lane);
+}
+
+// Selector operand of the chunk-pair summation MFMA.  The two chunk MFMAs of
+// a 16x16 block leave lane 16q+m holding P_c[m][4q+r], r < 4, for chunk
+// c = 0, 1; v_cvt_pk_f16_f32 packs (P_0, P_1)[m][4q+r] into dword r of an
+// f16x8 X (elements 2r, 2r+1).  With X as the hardware B operand and this
+// 0/1 matrix as A (lane 16q+i, element e: 1 when 4q + e/2 == i),
+//   D[i][m] = sum over q, e of A[16q+i][e] * X[16q+m][e]
+//           = H_0[m][i] + H_1[m][i]
+// lands in the accumulator layout of the chunk MFMAs, so
+// S = mfma(sel, X, S) adds both FP16-rounded partials to the FP32 sum with
+// exact products.  On gfx950 this costs one MFMA per chunk pair and overlaps
+// the VALU rounding, where summing with v_dot2_f32_f16 stalls the matrix pipe.
+// (An inf partial also leaves 0 * inf = NaN in other elements of its 16x16
+// block: the tile is flagged either way and recomputed whole.)
+__device__ __forceinline__ f16x8 chunk_pair_selector(int lane) {
+  const int q = lane >> 4, i = lane & 15;
+  f16x8 s;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s[e] = (4 * q + (e >> 1) == i) ? (f16)1.0f : (f16)0.0f;
+  return s;
+}
+
+__device__ __forceinline__ f16x8 round_pair(const f32x4& p0, const f32x4& p1) {
+  f16x8 x;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const f32x2 pr = {p0[r], p1[r]};
+    const f16x2 h = __builtin_convertvector(pr, f16x2);  // v_cvt_pk_f16_f32: RNE, inf past 65504
+    x[2 * r] = h[0];
+    x[2 * r + 1] = h[1];
+  }
+  return x;
+}
+
 template <class C, bool CHUNKED>
 __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, int wn, int lane,
                                               f32x4 (&acc)[C::FM][C::FN]) {
@@ -241,34 +286,49 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
   for (int i = 0; i < C::FM; ++i)
 #pragma unroll
     for (int c = 0; c < 2; ++c) af[i][c] = read_kc<C>(as, wm * C::WTM + 16 * i + r16, 4 * c + g);
-  const f16x2 ones = {(f16)1.0f, (f16)1.0f};
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  if (!CHUNKED) {
 #pragma unroll
-  for (int j = 0; j < C::FN; ++j) {
-    f16x8 bf[2];
+    for (int j = 0; j < C::FN; ++j) {
+      const f16x8 b0 = read_b<C>(bs, wn, j, 0, lane), b1 = read_b<C>(bs, wn, j, 1, lane);
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      if (C::BL == kKC)
-        bf[c] = read_kc<C>(bs, wn * C::WTN + 16 * j + r16, 4 * c + g);
-      else
-        bf[c] = read_nc<C>(bs, wn * C::WTN + 16 * j, c, lane);
-    }
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i) {
-      // operands swapped (b first) so lane l receives C[row l%16][4 consecutive columns]
-      if (CHUNKED) {
-        const f32x4 p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[0], af[i][0], zero, 0, 0, 0);
-        const f32x4 p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[1], af[i][1], zero, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const f32x2 pr = {p0[r], p1[r]};
-          const f16x2 h = __builtin_convertvector(pr, f16x2);  // v_cvt_pk_f16_f32, RNE
-          acc[i][j][r] = __builtin_amdgcn_fdot2(h, ones, acc[i][j][r], false);
-        }
-      } else {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[0], af[i][0], acc[i][j], 0, 0, 0);
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[1], af[i][1], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < C::FM; ++i) {
+        // operands swapped (b first) so lane l receives C[row l%16][4 consecutive columns]
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b0, af[i][0], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b1, af[i][1], acc[i][j], 0, 0, 0);
       }
+    }
+    return;
+  }
+  // Chunked: blocks t = 0 .. FM*FN-1 (i = t % FM fastest), software
+  // pipelined three deep: step t issues the two chunk MFMAs of block t, rounds
+  // the partials of block t-1 and sums block t-2 with the selector MFMA, so
+  // no instruction waits on the MFMA that produced its operand.
+  constexpr int T = C::FM * C::FN;
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  const f16x8 sel = chunk_pair_selector(lane);  // loop invariant: hoisted out of the K loop
+  f16x8 bcur[2], bnext[2];
+  bcur[0] = read_b<C>(bs, wn, 0, 0, lane);
+  bcur[1] = read_b<C>(bs, wn, 0, 1, lane);
+  f32x4 p0[2], p1[2];
+  f16x8 x[2];
+#pragma unroll
+  for (int t = 0; t < T + 2; ++t) {
+    const int i = t % C::FM, j = t / C::FM;
+    if (t < T && i == 0 && j + 1 < C::FN) {
+      bnext[0] = read_b<C>(bs, wn, j + 1, 0, lane);
+      bnext[1] = read_b<C>(bs, wn, j + 1, 1, lane);
+    }
+    if (t < T) p0[t & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bcur[0], af[i][0], zero, 0, 0, 0);
+    if (t >= 1 && t <= T) x[(t - 1) & 1] = round_pair(p0[(t - 1) & 1], p1[(t - 1) & 1]);
+    if (t < T) p1[t & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bcur[1], af[i][1], zero, 0, 0, 0);
+    if (t >= 2) {
+      const int u = t - 2;
+      acc[u % C::FM][u / C::FM] =
+          __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, x[u & 1], acc[u % C::FM][u / C::FM], 0, 0, 0);
+    }
+    if (t < T && i == C::FM - 1 && j + 1 < C::FN) {
+      bcur[0] = bnext[0];
+      bcur[1] = bnext[1];
     }
   }
 }
