@@ -130,6 +130,35 @@ def cpu_baseline(a, b, out_dtype, budget_s=20.0):
     return info, ref
 
 
+def sweep_tiles(names):
+    """Time every tile configuration (forced) on the given workloads, chunked,
+    next to the per-shape table's choice and hipBLASLt: the evidence behind
+    the table, as the reference's autotuner times its CONFIGS
+    (f16acc/kernel.py:16-19)."""
+    from f16acc_amd import _lib
+    from f16acc_amd.kernel import mm_tile, tile_config
+
+    for name in names:
+        M, N, K, layout, out_dtype = WORKLOADS[name]
+        _, _, a, b = make_inputs(M, N, K, layout)
+        flops = 2.0 * M * N * K
+        row = {"workload": name, "M": M, "N": N, "K": K, "b": layout, "table": tile_config(a, b)["tile"]}
+        for tile in _lib.TILES:
+            if tile_config(a, b, tile)["tile"] != tile:
+                continue  # the operands do not allow this tile
+            t = median_event_time(lambda: mm_tile(a, b, tile, out_dtype), iters=20, warmup=5)
+            row[tile] = round(flops / t / 1e12, 1)
+        import f16acc_amd
+
+        t = median_event_time(lambda: f16acc_amd.mm(a, b, out_dtype), iters=20, warmup=5)
+        row["mm"] = round(flops / t / 1e12, 1)  # the op as shipped: table choice, packing included
+        t = median_event_time(lambda: torch.mm(a, b), iters=20, warmup=5)
+        row["hipblaslt"] = round(flops / t / 1e12, 1)
+        print(json.dumps(row), flush=True)
+        del a, b
+        torch.cuda.empty_cache()
+
+
 def copy_reference(steps, warmup, nbytes=1 << 30):
     """A plain device copy of known size (1 GiB read + 1 GiB written per step):
     the calibration for rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
@@ -147,6 +176,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="gemm4096", choices=sorted(WORKLOADS) + ["copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and oracle comparison")
+    ap.add_argument("--sweep-tiles", nargs="*", metavar="WORKLOAD",
+                    help="time every tile configuration on these workloads (all if none given) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (a GEMM shards by M or N "
@@ -155,6 +186,8 @@ def main():
 
     if args.workload == "copy":
         return copy_reference(args.steps, args.warmup)
+    if args.sweep_tiles is not None:
+        return sweep_tiles(args.sweep_tiles or sorted(WORKLOADS))
 
     import f16acc_amd
     from f16acc_amd.kernel import tile_config

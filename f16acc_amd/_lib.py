@@ -22,8 +22,16 @@ gemm = _dll.f16acc_gemm
 gemm.argtypes = [_vp, _vp, _vp, _vp] + [_i64] * 9 + [_int, _int, _vp]
 gemm.restype = _int
 
+gemm_tile = _dll.f16acc_gemm_tile
+gemm_tile.argtypes = [_vp, _vp, _vp, _vp] + [_i64] * 9 + [_int, _int, _vp, _int]
+gemm_tile.restype = _int
+
+pack = _dll.f16acc_pack
+pack.argtypes = [_vp, _vp] + [_i64] * 6 + [_vp]
+pack.restype = _int
+
 tile_config = _dll.f16acc_tile_config
-tile_config.argtypes = [_i64] * 7 + [_vp, _vp, _PI, _PI, _P64, _P64, _PI, _PI]
+tile_config.argtypes = [_i64] * 7 + [_vp, _vp, _int, _PI, _PI, _PI, _P64, _P64, _PI, _PI]
 tile_config.restype = _int
 
 block_tile = _dll.f16acc_block_tile
@@ -39,10 +47,17 @@ abi_version.argtypes = []
 abi_version.restype = _int
 
 # Exported symbol names, as declared in include/f16acc.h.
-EXPORTS = ("f16acc_gemm", "f16acc_tile_config", "f16acc_block_tile", "f16acc_strerror", "f16acc_abi_version")
+EXPORTS = ("f16acc_gemm", "f16acc_gemm_tile", "f16acc_pack", "f16acc_tile_config", "f16acc_block_tile", "f16acc_strerror",
+           "f16acc_abi_version")
+ABI_VERSION = 2
 
 OUT_F16, OUT_F32 = 0, 1
 E_ARG, E_UNSUPPORTED = -1, -2
+TILES = ("256x256", "256x128", "128x256", "128x128", "generic")  # F16ACC_TILE_* ids
+TILE_GENERIC = 4
+
+if abi_version() != ABI_VERSION:
+    raise ImportError(f"{LIB} has ABI version {abi_version()}, this package needs {ABI_VERSION}: rebuild it")
 
 
 def check(rc):

@@ -104,9 +104,9 @@ __device__ __forceinline__ int nc_swz(int krow) { return 2 * (krow & 3) + 8 * ((
 // Layout of B in LDS.
 enum BLayout { kKC = 0, kNC = 1 };
 
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int BL_>
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int NS_, int BL_>
 struct Cfg {
-  static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, BL = BL_;
+  static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, NS = NS_, BL = BL_;
   static constexpr int T = 64 * WAVES_M * WAVES_N;
   static constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;  // wave tile
   static constexpr int FM = WTM / 16, FN = WTN / 16;            // 16x16 MFMA blocks per wave
@@ -119,6 +119,8 @@ struct Cfg {
   static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave tile must be whole 16x16 blocks");
   static_assert(BM * 8 % T == 0 && BN * 8 % T == 0, "stage must split evenly over threads");
   static_assert(BL == kKC || BN >= 128, "NC swizzle needs at least 16 units per k-row");
+  static_assert(NS >= 2 && NS * STAGE <= 160 * 1024, "LDS ring must fit the 160 KiB of a CU");
+  static_assert((NS - 2) * (LA + LB) <= 63, "outstanding loads must fit vmcnt");
 };
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -154,10 +156,14 @@ __device__ __forceinline__ void lds_dma16(const i32x4& srd, int lds, int voff) {
 }
 #pragma clang diagnostic pop
 
-__device__ __forceinline__ void wait_vm0() {
-  // s_waitcnt vmcnt(0), other counters left alone (gfx9 encoding)
-  __builtin_amdgcn_s_waitcnt(0x0f70);
+// s_waitcnt vmcnt(N), other counters left alone (gfx9 encoding: vmcnt bits
+// [3:0] and [15:14], expcnt [6:4] = 7, lgkmcnt [11:8] = 15).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
 }
+__device__ __forceinline__ void wait_vm0() { wait_vm<0>(); }
 
 // ---------------------------------------------------------------------------
 // Per-thread stage loader state for the direct-to-LDS fast path.
@@ -333,21 +339,35 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
   }
 }
 
-// Whole K loop of the fast path: two LDS stages, the copy of stage s+1 in
-// flight while stage s is multiplied.
+// Whole K loop of the fast path: an NS-stage LDS ring.  The copies of the
+// next NS-1 stages are in flight while a stage is multiplied: at step s the
+// wave waits until its own copies of stage s have landed (vmcnt counts the
+// later stages' copies that may stay outstanding), the barrier makes every
+// wave's copies visible and retires all reads of the slot stage s+NS-1 will
+// overwrite, then that copy is issued and stage s is multiplied.
 template <class C, bool CHUNKED>
 __device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t n0, char LDS_AS* smem,
                                             FastLoader<C>& ld, int tid, int wave, int wm, int wn, int lane,
                                             f32x4 (&acc)[C::FM][C::FN]) {
   const int64_t nsteps = (p.K + kStageK - 1) / kStageK;
   if (nsteps == 0) return;
-  ld.issue(p, m0, n0, 0, smem, wave);
+#pragma unroll
+  for (int s0 = 0; s0 < C::NS - 1; ++s0)
+    if (s0 < nsteps) ld.issue(p, m0, n0, (int64_t)s0 * kStageK, smem + s0 * C::STAGE, wave);
+  int slot = 0;
   for (int64_t s = 0; s < nsteps; ++s) {
-    wait_vm0();
+    if (s + C::NS - 2 < nsteps)
+      wait_vm<(C::NS - 2) * (C::LA + C::LB)>();
+    else
+      wait_vm0();
     __syncthreads();
-    char LDS_AS* cur = smem + (s & 1) * C::STAGE;
-    if (s + 1 < nsteps) ld.issue(p, m0, n0, (s + 1) * kStageK, smem + ((s + 1) & 1) * C::STAGE, wave);
-    compute_stage<C, CHUNKED>(cur, wm, wn, lane, acc);
+    const int64_t nxt = s + C::NS - 1;
+    if (nxt < nsteps) {
+      const int nslot = slot == 0 ? C::NS - 1 : slot - 1;  // (s + NS - 1) % NS
+      ld.issue(p, m0, n0, nxt * kStageK, smem + nslot * C::STAGE, wave);
+    }
+    compute_stage<C, CHUNKED>(smem + slot * C::STAGE, wm, wn, lane, acc);
+    slot = slot + 1 == C::NS ? 0 : slot + 1;
   }
   __syncthreads();  // LDS free for a redo pass
 }
@@ -357,7 +377,7 @@ __device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t
 template <class C>
 __device__ __forceinline__ void stage_generic(const Params& p, int64_t m0, int64_t n0, int64_t kbase,
                                               char LDS_AS* stage, int tid) {
-#pragma unroll
+#pragma unroll 2
   for (int j = 0; j < C::LA; ++j) {
     const int s = j * C::T + tid, row = s >> 3, u = (s & 7) ^ kc_swz(row);
     const int64_t m = m0 + row;
@@ -369,7 +389,7 @@ __device__ __forceinline__ void stage_generic(const Params& p, int64_t m0, int64
     }
     *(f16x8 LDS_AS*)(stage + s * 16) = v;
   }
-#pragma unroll
+#pragma unroll 2
   for (int j = 0; j < C::LB; ++j) {
     const int s = j * C::T + tid, row = s >> 3, u = (s & 7) ^ kc_swz(row);
     const int64_t n = n0 + row;
@@ -433,9 +453,12 @@ __device__ __forceinline__ void store_tile(const Params& p, int64_t m0, int64_t 
 }
 
 // One kernel body for both families: FAST selects the direct-to-LDS loader.
+// amdgpu_waves_per_eu(2) caps a wave at 256 registers, which keeps every MFMA
+// in its VGPR form: the chunk partials are read by VALU conversions, and an
+// AGPR destination would cost a v_accvgpr_read per register.
 template <class C, bool FAST, bool CHUNKED, bool OUT32>
-__global__ __launch_bounds__(C::T) void gemm_kernel(Params p) {
-  __shared__ __attribute__((aligned(1024))) char smem_raw[FAST ? 2 * C::STAGE : C::STAGE];
+__global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(Params p) {
+  __shared__ __attribute__((aligned(1024))) char smem_raw[FAST ? C::NS * C::STAGE : C::STAGE];
   __shared__ int tile_bad;
   char LDS_AS* smem = (char LDS_AS*)smem_raw;
 
@@ -491,19 +514,57 @@ __global__ __launch_bounds__(C::T) void gemm_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------
-// Host side: per-shape tile table and launch.
+// Operand packing.  The fast kernels copy 16-byte units straight into LDS,
+// so rows must start 16-byte aligned and K (or N for a row-major b) must be
+// a multiple of 8.  Operands that miss this (odd K such as 8961, odd
+// strides, offset views) are copied once into a padded contiguous buffer:
+// dst[r][c] = src[r * s_r + c * s_c] for r < rows, c < cols, and 0 in the
+// padding up to rows_pad x ld.  Zero padding along K adds exact zeros to the
+// last chunk's sum, so the chunk semantics are unchanged.  One thread writes
+// one 16-byte unit; consecutive threads read consecutive source elements
+// when s_c == 1.  A transposing copy (s_r == 1: a row-major b packed into
+// the K-contiguous layout) numbers the units column-major instead, so that
+// consecutive threads read consecutive source elements there too.
 // ---------------------------------------------------------------------------
-using CfgL_KC = Cfg<256, 256, 4, 2, kKC>;  // 8 waves, 64x128 per wave, 128 KiB LDS
-using CfgL_NC = Cfg<256, 256, 4, 2, kNC>;
-using CfgM_KC = Cfg<128, 128, 2, 2, kKC>;  // 4 waves, 64x64 per wave, 64 KiB LDS
-using CfgM_NC = Cfg<128, 128, 2, 2, kNC>;
-using CfgG = Cfg<128, 128, 2, 2, kKC>;     // generic gather path (single LDS stage)
+template <bool COLUMN_MAJOR_UNITS>
+__global__ __launch_bounds__(256) void pack_kernel(const f16* __restrict__ src, f16* __restrict__ dst,
+                                                  int64_t rows, int64_t cols, int64_t s_r, int64_t s_c,
+                                                  int64_t rows_pad, int64_t ld) {
+  const int64_t units_per_row = ld / 8;
+  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (u >= rows_pad * units_per_row) return;
+  const int64_t r = COLUMN_MAJOR_UNITS ? u % rows_pad : u / units_per_row;
+  const int64_t c0 = 8 * (COLUMN_MAJOR_UNITS ? u / rows_pad : u % units_per_row);
+  f16x8 v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int64_t c = c0 + e;
+    v[e] = (r < rows && c < cols) ? src[r * s_r + c * s_c] : (f16)0.0f;
+  }
+  *(f16x8*)(dst + r * ld + c0) = v;
+}
 
-enum Family { kFast = 0, kGeneric = 1 };
+// ---------------------------------------------------------------------------
+// Host side: tile table, per-shape choice and launch.
+// ---------------------------------------------------------------------------
+// Tile configurations (ids are the F16ACC_TILE_* values of include/f16acc.h).
+//   id  tile     waves  wave tile  LDS ring      workgroups per CU (LDS)
+//   0   256x256  8      64x128     2 x 64 KiB    1
+//   1   256x128  8      64x64      3 x 48 KiB    1
+//   2   128x256  8      64x64      3 x 48 KiB    1
+//   3   128x128  4      64x64      2 x 32 KiB    2
+//   4   128x128  4      64x64      1 x 32 KiB    generic strided gather path
+template <int BL> using Cfg0 = Cfg<256, 256, 4, 2, 2, BL>;
+template <int BL> using Cfg1 = Cfg<256, 128, 4, 2, 3, BL>;
+template <int BL> using Cfg2 = Cfg<128, 256, 2, 4, 3, BL>;
+template <int BL> using Cfg3 = Cfg<128, 128, 2, 2, 2, BL>;
+using CfgG = Cfg<128, 128, 2, 2, 2, kKC>;
 
-struct Choice {
-  int bm, bn, family, threads, blayout;
+struct TileInfo {
+  int bm, bn, threads, per_cu;
 };
+constexpr TileInfo kTiles[F16ACC_NUM_TILES] = {
+    {256, 256, 512, 1}, {256, 128, 512, 1}, {128, 256, 512, 1}, {128, 128, 256, 2}, {128, 128, 256, 2}};
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -515,8 +576,8 @@ inline int cu_count() {
 }
 
 // Which loader the operands allow.  blayout: kKC / kNC, or -1 for generic.
-inline int fast_layout(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
-                       const void* a, const void* b, int bm, int bn) {
+inline int fast_layout(int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, const void* a,
+                       const void* b, int bm, int bn) {
   const bool a_ok = (sak == 1 || K <= 1) && sam % 8 == 0 && ((uintptr_t)a % 16) == 0 && K % 8 == 0 &&
                     (int64_t)bm * sam * 2 + 4 * kStageK < kOob;
   if (!a_ok) return -1;
@@ -527,18 +588,50 @@ inline int fast_layout(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak
                     (int64_t)kStageK * sbk * 2 + 2 * bn < kOob;
   if (b_nc) return kNC;
   return -1;
-  (void)M;
 }
 
+// Relative throughput of one CU on each fast tile (its chunked MFMA work
+// rate, 128x128 running two workgroups per CU), from tile sweeps on MI355X
+// (4096^3, 8192^3 and the Qwen2.5-1.5B layer shapes), used to compare tile
+// choices for a shape.  Workgroups spread over the CUs, so a CU ends up with
+// ceil(tiles / CUs) tiles:
+//   estimated time = ceil(tiles / CUs) x tile area / rate.
+// A 256x256 workgroup holds its CU alone, so with fewer than two tiles per
+// CU nothing hides its load latency and barrier waits: its rate drops to
+// ~0.78 of the loaded rate (4096^3: 655 against 856 TFLOPS at 8192^3).
+constexpr double kTileRate[4] = {1.00, 0.90, 0.92, 0.94};
+constexpr double kLoneBigTile = 0.78;
+
+// The per-shape table: the fast tile with the smallest estimated time.
+// Ties keep the larger tile.
+inline int choose_tile(int64_t M, int64_t N, int cus) {
+  int best = 0;
+  double best_t = 0;
+  for (int id = 0; id < 4; ++id) {
+    const TileInfo& t = kTiles[id];
+    const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
+    double rate = kTileRate[id];
+    if (id == 0 && tiles < 2 * (int64_t)cus) rate *= kLoneBigTile;
+    const double est = (double)cdiv(tiles, cus) * t.bm * t.bn / rate;
+    if (id == 0 || est < best_t * 0.999) {
+      best = id;
+      best_t = est;
+    }
+  }
+  return best;
+}
+
+struct Choice {
+  int tile, family, blayout;
+};
+
 inline Choice choose(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
-                     const void* a, const void* b) {
-  // Big tiles when they alone fill every CU; otherwise 128x128 (4x the tiles).
-  const int cus = cu_count();
-  const bool big = cdiv(M, 256) * cdiv(N, 256) >= cus;
-  const int bm = big ? 256 : 128, bn = bm;
-  const int bl = fast_layout(M, N, K, sam, sak, sbk, sbn, a, b, bm, bn);
-  if (bl < 0) return Choice{CfgG::BM, CfgG::BN, kGeneric, CfgG::T, kKC};
-  return Choice{bm, bn, kFast, big ? CfgL_KC::T : CfgM_KC::T, bl};
+                     const void* a, const void* b, int forced_tile) {
+  const int id = forced_tile >= 0 ? forced_tile : choose_tile(M, N, cu_count());
+  if (id == F16ACC_TILE_GENERIC) return Choice{id, F16ACC_FAMILY_GENERIC, kKC};
+  const int bl = fast_layout(N, K, sam, sak, sbk, sbn, a, b, kTiles[id].bm, kTiles[id].bn);
+  if (bl < 0) return Choice{F16ACC_TILE_GENERIC, F16ACC_FAMILY_GENERIC, kKC};
+  return Choice{id, F16ACC_FAMILY_FAST, bl};
 }
 
 template <class C, bool FAST>
@@ -558,11 +651,50 @@ hipError_t launch_cfg(const Params& p, int out32, int chunked, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <template <int> class CF>
+hipError_t launch_fast(const Params& p, int blayout, int out32, int chunked, hipStream_t st) {
+  return blayout == kKC ? launch_cfg<CF<kKC>, true>(p, out32, chunked, st)
+                        : launch_cfg<CF<kNC>, true>(p, out32, chunked, st);
+}
+
+int gemm_impl(const void* a, const void* b, void* c, uint8_t* tile_flags, int64_t M, int64_t N, int64_t K,
+              int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int out_dtype,
+              int chunked, void* stream, int forced_tile) {
+  if (M < 0 || N < 0 || K < 0) return F16ACC_E_ARG;
+  if (out_dtype != F16ACC_OUT_F16 && out_dtype != F16ACC_OUT_F32) return F16ACC_E_ARG;
+  if (chunked != 0 && chunked != 1) return F16ACC_E_ARG;
+  if (forced_tile < -1 || forced_tile >= F16ACC_NUM_TILES) return F16ACC_E_ARG;
+  if (M == 0 || N == 0) return 0;  // nothing to write (Triton skips an empty grid too)
+  if (!c || (K > 0 && (!a || !b))) return F16ACC_E_ARG;
+  const Choice ch = choose(M, N, K, sam, sak, sbk, sbn, a, b, forced_tile);
+  Params p;
+  p.a = (const f16*)a;
+  p.b = (const f16*)b;
+  p.c = c;
+  p.flags = tile_flags;
+  p.M = M; p.N = N; p.K = K;
+  p.sam = sam; p.sak = sak; p.sbk = sbk; p.sbn = sbn; p.scm = scm; p.scn = scn;
+  p.tiles_m = cdiv(M, kTiles[ch.tile].bm);
+  p.tiles_n = cdiv(N, kTiles[ch.tile].bn);
+  const int esize = out_dtype == F16ACC_OUT_F32 ? 4 : 2;
+  p.vec_store = scn == 1 && (scm * esize) % 16 == 0 && ((uintptr_t)c % 16) == 0;
+  if (p.tiles_m * p.tiles_n > 0x7fffffff) return F16ACC_E_UNSUPPORTED;
+  const int out32 = out_dtype == F16ACC_OUT_F32;
+  hipStream_t st = (hipStream_t)stream;
+  switch (ch.tile) {
+    case 0: return (int)launch_fast<Cfg0>(p, ch.blayout, out32, chunked, st);
+    case 1: return (int)launch_fast<Cfg1>(p, ch.blayout, out32, chunked, st);
+    case 2: return (int)launch_fast<Cfg2>(p, ch.blayout, out32, chunked, st);
+    case 3: return (int)launch_fast<Cfg3>(p, ch.blayout, out32, chunked, st);
+    default: return (int)launch_cfg<CfgG, false>(p, out32, chunked, st);
+  }
+}
+
 }  // namespace
 
 extern "C" {
 
-int f16acc_abi_version(void) { return 1; }
+int f16acc_abi_version(void) { return 2; }
 
 const char* f16acc_strerror(int code) {
   if (code == 0) return "success";
@@ -580,52 +712,50 @@ int f16acc_block_tile(int64_t block, int64_t tiles_m, int64_t tiles_n, int64_t* 
 }
 
 int f16acc_tile_config(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
-                       const void* a, const void* b, int* bm, int* bn, int64_t* tiles_m, int64_t* tiles_n,
-                       int* family, int* threads) {
-  if (M < 0 || N < 0 || K < 0) return F16ACC_E_ARG;
-  const Choice ch = choose(M, N, K, sam, sak, sbk, sbn, a, b);
-  if (bm) *bm = ch.bm;
-  if (bn) *bn = ch.bn;
-  if (tiles_m) *tiles_m = cdiv(M, ch.bm);
-  if (tiles_n) *tiles_n = cdiv(N, ch.bn);
+                       const void* a, const void* b, int forced_tile, int* tile, int* bm, int* bn,
+                       int64_t* tiles_m, int64_t* tiles_n, int* family, int* threads) {
+  if (M < 0 || N < 0 || K < 0 || forced_tile < -1 || forced_tile >= F16ACC_NUM_TILES) return F16ACC_E_ARG;
+  const Choice ch = choose(M, N, K, sam, sak, sbk, sbn, a, b, forced_tile);
+  const TileInfo& t = kTiles[ch.tile];
+  if (tile) *tile = ch.tile;
+  if (bm) *bm = t.bm;
+  if (bn) *bn = t.bn;
+  if (tiles_m) *tiles_m = cdiv(M, t.bm);
+  if (tiles_n) *tiles_n = cdiv(N, t.bn);
   if (family) *family = ch.family;
-  if (threads) *threads = ch.threads;
+  if (threads) *threads = t.threads;
   return 0;
 }
 
 int f16acc_gemm(const void* a, const void* b, void* c, uint8_t* tile_flags, int64_t M, int64_t N, int64_t K,
                 int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int out_dtype,
                 int chunked, void* stream) {
-  if (M < 0 || N < 0 || K < 0) return F16ACC_E_ARG;
-  if (out_dtype != F16ACC_OUT_F16 && out_dtype != F16ACC_OUT_F32) return F16ACC_E_ARG;
-  if (chunked != 0 && chunked != 1) return F16ACC_E_ARG;
-  if (M == 0 || N == 0) return 0;  // nothing to write (Triton skips an empty grid too)
-  if (!c || (K > 0 && (!a || !b))) return F16ACC_E_ARG;
-  const Choice ch = choose(M, N, K, sam, sak, sbk, sbn, a, b);
-  Params p;
-  p.a = (const f16*)a;
-  p.b = (const f16*)b;
-  p.c = c;
-  p.flags = tile_flags;
-  p.M = M; p.N = N; p.K = K;
-  p.sam = sam; p.sak = sak; p.sbk = sbk; p.sbn = sbn; p.scm = scm; p.scn = scn;
-  p.tiles_m = cdiv(M, ch.bm);
-  p.tiles_n = cdiv(N, ch.bn);
-  const int esize = out_dtype == F16ACC_OUT_F32 ? 4 : 2;
-  p.vec_store = scn == 1 && (scm * esize) % 16 == 0 && ((uintptr_t)c % 16) == 0;
-  if (p.tiles_m * p.tiles_n > 0x7fffffff) return F16ACC_E_UNSUPPORTED;
-  const int out32 = out_dtype == F16ACC_OUT_F32;
-  hipStream_t st = (hipStream_t)stream;
-  hipError_t e;
-  if (ch.family == kGeneric)
-    e = launch_cfg<CfgG, false>(p, out32, chunked, st);
-  else if (ch.bm == 256)
-    e = ch.blayout == kKC ? launch_cfg<CfgL_KC, true>(p, out32, chunked, st)
-                          : launch_cfg<CfgL_NC, true>(p, out32, chunked, st);
+  return gemm_impl(a, b, c, tile_flags, M, N, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked, stream, -1);
+}
+
+int f16acc_pack(const void* src, void* dst, int64_t rows, int64_t cols, int64_t s_r, int64_t s_c,
+                int64_t rows_pad, int64_t ld, void* stream) {
+  if (rows < 0 || cols < 0 || rows_pad < rows || ld < cols || ld % 8 != 0) return F16ACC_E_ARG;
+  if (rows_pad == 0 || ld == 0) return 0;
+  if (!dst || ((uintptr_t)dst % 16) != 0 || (rows > 0 && cols > 0 && !src)) return F16ACC_E_ARG;
+  const int64_t units = rows_pad * (ld / 8);
+  const int64_t blocks = cdiv(units, 256);
+  if (blocks > 0x7fffffff) return F16ACC_E_UNSUPPORTED;
+  const bool col_units = s_r == 1 && s_c != 1;
+  if (col_units)
+    hipLaunchKernelGGL(pack_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                       (const f16*)src, (f16*)dst, rows, cols, s_r, s_c, rows_pad, ld);
   else
-    e = ch.blayout == kKC ? launch_cfg<CfgM_KC, true>(p, out32, chunked, st)
-                          : launch_cfg<CfgM_NC, true>(p, out32, chunked, st);
-  return (int)e;
+    hipLaunchKernelGGL(pack_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                       (const f16*)src, (f16*)dst, rows, cols, s_r, s_c, rows_pad, ld);
+  return (int)hipGetLastError();
+}
+
+int f16acc_gemm_tile(const void* a, const void* b, void* c, uint8_t* tile_flags, int64_t M, int64_t N, int64_t K,
+                     int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int out_dtype,
+                     int chunked, void* stream, int tile) {
+  if (tile < 0) return F16ACC_E_ARG;
+  return gemm_impl(a, b, c, tile_flags, M, N, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked, stream, tile);
 }
 
 }  // extern "C"

@@ -5,7 +5,9 @@ arguments, the same ValueError checks before any launch, a freshly allocated
 contiguous output, and no synchronisation.  The Triton `_gemm` / `_redo`
 launches are replaced by one call into libf16acc_amd.so (f16acc_gemm), which
 runs the main pass and the FP32 redo of overflowing tiles in one kernel on
-the current stream.
+the current stream.  Operands the fast kernels cannot read directly (rows not
+16-byte aligned, e.g. K = 8961; odd strides) are first copied by the
+library's pack kernel into zero-padded buffers that torch allocates.
 """
 
 import ctypes
@@ -15,6 +17,10 @@ import torch
 from . import _lib
 
 _OUT = {torch.float16: _lib.OUT_F16, torch.float32: _lib.OUT_F32}
+
+# Below this many multiply-adds the generic gather kernel beats a pack + fast
+# kernel (the copy's launch and traffic are not repaid).
+PACK_MIN_MACS = 1 << 24
 
 
 def _validate(a, b, out_dtype):
@@ -43,46 +49,117 @@ def mm(a, b, out_dtype=torch.float16, chunked=True):
     c = torch.empty(M, N, device=a.device, dtype=out_dtype)
     if M == 0 or N == 0:
         return c
+    a, b, K = _operands(a, b, M, N, K)
     _launch(a, b, c, None, M, N, K, chunked)
     return c
 
 
-def mm_flags(a, b, out_dtype=torch.float16, chunked=True):
+def _fast_a(a, K):
+    """a [M, K] as the fast kernels read it: K-contiguous 16-byte aligned rows."""
+    return K % 8 == 0 and (a.stride(1) == 1 or K <= 1) and a.stride(0) % 8 == 0 and a.data_ptr() % 16 == 0
+
+
+def _fast_b(b, K, N):
+    """b [K, N]: K-contiguous columns (w.t()) or N-contiguous rows, 16-byte aligned."""
+    if b.data_ptr() % 16:
+        return False
+    kc = K % 8 == 0 and (b.stride(0) == 1 or K <= 1) and b.stride(1) % 8 == 0
+    nc = N % 8 == 0 and (b.stride(1) == 1 or N <= 1) and b.stride(0) % 8 == 0
+    return kc or nc
+
+
+def _pack(src, rows, cols, s_r, s_c, ld):
+    """Zero-padded contiguous [rows, ld] copy of a strided fp16 matrix (f16acc_pack)."""
+    dst = torch.empty(rows, ld, device=src.device, dtype=torch.float16)
+    stream = torch.cuda.current_stream(src.device).cuda_stream
+    _lib.check(_lib.pack(src.data_ptr(), dst.data_ptr(), rows, cols, s_r, s_c, rows, ld, stream))
+    return dst
+
+
+def _operands(a, b, M, N, K, tile=None):
+    """The operands the GEMM runs on: a and b themselves when the fast kernels
+    can read them (or the problem is too small to repay a copy, or the
+    generic tile is forced), else packed copies with K padded to a multiple
+    of 8 by zeros: a as [M, Kp] rows, b as the K-contiguous [Kp, N] view of an
+    [N, Kp] buffer.  Returns (a, b, K) for the launch."""
+    if K == 0 or tile == "generic" or (tile is None and M * N * K < PACK_MIN_MACS):
+        return a, b, K
+    ok_a, ok_b = _fast_a(a, K), _fast_b(b, K, N)
+    if ok_a and ok_b:
+        return a, b, K
+    Kp = -(-K // 8) * 8
+    if Kp != K or not ok_a:
+        with torch.cuda.device(a.device):
+            a = _pack(a, M, K, a.stride(0), a.stride(1), Kp)
+    if Kp != K or not ok_b:
+        with torch.cuda.device(b.device):
+            b = _pack(b, N, K, b.stride(1), b.stride(0), Kp).t()  # element (n, k) = b[k][n]
+    return a, b, Kp
+
+
+def mm_flags(a, b, out_dtype=torch.float16, chunked=True, tile=None):
     """mm plus the per-tile redo flags (uint8 [tiles_m, tiles_n]): 1 where the
     tile's chunked FP32 sum held inf/NaN and was recomputed in FP32.  Same
-    checks as mm; used by tests and benches to see which tiles were redone."""
+    checks as mm; used by tests and benches to see which tiles were redone.
+    tile: None for the per-shape table's choice, or a name of _lib.TILES to
+    force that configuration (tuning, as the reference's autotuner does)."""
     _validate(a, b, out_dtype)
     M, K = a.shape
     N = b.shape[1]
-    cfg = tile_config(a, b)
     c = torch.empty(M, N, device=a.device, dtype=out_dtype)
+    if M and N:
+        a, b, K = _operands(a, b, M, N, K, tile)
+    cfg = tile_config(a, b, tile)
     flags = torch.zeros(cfg["tiles_m"], cfg["tiles_n"], device=a.device, dtype=torch.uint8)
     if M and N:
-        _launch(a, b, c, flags, M, N, K, chunked)
+        _launch(a, b, c, flags, M, N, K, chunked, _tile_id(tile))
     return c, flags
 
 
-def tile_config(a, b):
-    """The per-shape tile choice the library makes for a @ b (replaces the
-    reference's autotuned best_config, kernel.py:16-19, 101-102)."""
+def mm_tile(a, b, tile, out_dtype=torch.float16, chunked=True):
+    """mm with the tile configuration forced to `tile` (a name of _lib.TILES)."""
+    _validate(a, b, out_dtype)
     M, K = a.shape
     N = b.shape[1]
-    bm, bn, fam, thr = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    c = torch.empty(M, N, device=a.device, dtype=out_dtype)
+    if M and N:
+        a, b, K = _operands(a, b, M, N, K, tile)
+        _launch(a, b, c, None, M, N, K, chunked, _tile_id(tile))
+    return c
+
+
+def _tile_id(tile):
+    if tile is None:
+        return -1
+    if tile not in _lib.TILES:
+        raise ValueError(f"tile must be one of {_lib.TILES}, not {tile!r}")
+    return _lib.TILES.index(tile)
+
+
+def tile_config(a, b, tile=None):
+    """The per-shape tile choice the library makes for a @ b (replaces the
+    reference's autotuned best_config, kernel.py:16-19, 101-102), or what a
+    forced `tile` resolves to for these operands."""
+    M, K = a.shape
+    N = b.shape[1]
+    tid, bm, bn, fam, thr = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     tm, tn = ctypes.c_int64(), ctypes.c_int64()
     _lib.check(_lib.tile_config(M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
-                                a.data_ptr(), b.data_ptr(), ctypes.byref(bm), ctypes.byref(bn),
-                                ctypes.byref(tm), ctypes.byref(tn), ctypes.byref(fam), ctypes.byref(thr)))
-    return {"bm": bm.value, "bn": bn.value, "tiles_m": tm.value, "tiles_n": tn.value,
-            "family": ("fast", "generic")[fam.value], "threads": thr.value}
+                                a.data_ptr(), b.data_ptr(), _tile_id(tile), ctypes.byref(tid), ctypes.byref(bm),
+                                ctypes.byref(bn), ctypes.byref(tm), ctypes.byref(tn), ctypes.byref(fam),
+                                ctypes.byref(thr)))
+    return {"tile": _lib.TILES[tid.value], "bm": bm.value, "bn": bn.value, "tiles_m": tm.value,
+            "tiles_n": tn.value, "family": ("fast", "generic")[fam.value], "threads": thr.value}
 
 
-def _launch(a, b, c, flags, M, N, K, chunked):
+def _launch(a, b, c, flags, M, N, K, chunked, tile=-1):
     dev = a.device
     if torch.cuda.current_device() != dev.index:
         with torch.cuda.device(dev):
-            return _launch(a, b, c, flags, M, N, K, chunked)
+            return _launch(a, b, c, flags, M, N, K, chunked, tile)
     stream = torch.cuda.current_stream(dev).cuda_stream
-    rc = _lib.gemm(a.data_ptr(), b.data_ptr(), c.data_ptr(), flags.data_ptr() if flags is not None else None,
-                   M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1),
-                   _OUT[c.dtype], int(bool(chunked)), stream)
+    args = (a.data_ptr(), b.data_ptr(), c.data_ptr(), flags.data_ptr() if flags is not None else None,
+            M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1),
+            _OUT[c.dtype], int(bool(chunked)), stream)
+    rc = _lib.gemm(*args) if tile < 0 else _lib.gemm_tile(*args, tile)
     _lib.check(rc)

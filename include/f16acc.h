@@ -24,6 +24,18 @@ extern "C" {
 #define F16ACC_E_ARG (-1)        /* negative size, null pointer with work to do, bad enum */
 #define F16ACC_E_UNSUPPORTED (-2) /* a layout / extent this build cannot address */
 
+/* Tile configurations of the per-shape table (f16acc_tile_config reports
+ * which one a problem uses; f16acc_gemm_tile forces one). */
+#define F16ACC_TILE_256x256 0
+#define F16ACC_TILE_256x128 1
+#define F16ACC_TILE_128x256 2
+#define F16ACC_TILE_128x128 3
+#define F16ACC_TILE_GENERIC 4 /* 128x128, any strides, element gather */
+#define F16ACC_NUM_TILES 5
+
+#define F16ACC_FAMILY_FAST 0    /* direct global -> LDS copies of 16-byte units */
+#define F16ACC_FAMILY_GENERIC 1 /* strided element gather through registers */
+
 /*
  * c[M,N] = a[M,K] @ b[K,N]; a and b binary16, c binary16 or binary32.
  *
@@ -65,15 +77,46 @@ int f16acc_gemm(const void* a, const void* b, void* c, uint8_t* tile_flags,
  * The tile configuration f16acc_gemm picks for a problem: replaces the
  * reference's autotuned CONFIGS table and best_config handoff
  * (f16acc/kernel.py:16-19, 63, 101-102) with a fixed per-shape table.
- * Writes the workgroup tile (bm x bn), the tile grid, the kernel family
- * (0 = direct-to-LDS fast path, 1 = generic strided path) and the number of
- * threads per workgroup.  Any output pointer may be NULL.
+ * forced_tile = -1 asks for the table's choice; an F16ACC_TILE_* value asks
+ * what f16acc_gemm_tile would run with that tile (a fast tile the operands'
+ * strides or alignment do not allow falls back to F16ACC_TILE_GENERIC).
+ * Writes the tile id, the workgroup tile (bm x bn), the tile grid, the
+ * kernel family (F16ACC_FAMILY_*) and the threads per workgroup.  Any output
+ * pointer may be NULL.
  */
 int f16acc_tile_config(int64_t M, int64_t N, int64_t K,
                        int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
-                       const void* a, const void* b,
-                       int* bm, int* bn, int64_t* tiles_m, int64_t* tiles_n,
+                       const void* a, const void* b, int forced_tile,
+                       int* tile, int* bm, int* bn, int64_t* tiles_m, int64_t* tiles_n,
                        int* family, int* threads);
+
+/*
+ * f16acc_gemm with the tile configuration forced to `tile` (F16ACC_TILE_*)
+ * instead of the per-shape table's choice; same results up to the redo
+ * granularity (tile_flags follows the forced tile grid).  For tuning and
+ * benchmarking the table, as the reference's autotuner times every entry of
+ * CONFIGS on first use (f16acc/kernel.py:16-19, 63).
+ */
+int f16acc_gemm_tile(const void* a, const void* b, void* c, uint8_t* tile_flags,
+                     int64_t M, int64_t N, int64_t K,
+                     int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                     int64_t scm, int64_t scn,
+                     int out_dtype, int chunked, void* stream, int tile);
+
+/*
+ * Operand packing for the fast kernels: dst[r][c] = src[r*s_r + c*s_c] for
+ * r < rows, c < cols, zero elsewhere in the rows_pad x ld destination
+ * (contiguous, row stride ld; ld a multiple of 8, dst 16-byte aligned).
+ * The fast kernels need 16-byte aligned rows and K a multiple of 8; an
+ * operand that misses this (odd K, odd strides, offset views) is packed once
+ * with K padded by zeros (exact: zeros add nothing to a chunk's sum) and the
+ * GEMM runs on the copy.  The reference needs no counterpart: Triton's
+ * masked loads (f16acc/kernel.py:45-47) read any layout directly, at the
+ * cost this copy avoids.  The caller owns dst (the Python layer allocates it
+ * with torch).  Launches on `stream`; no synchronisation.
+ */
+int f16acc_pack(const void* src, void* dst, int64_t rows, int64_t cols,
+                int64_t s_r, int64_t s_c, int64_t rows_pad, int64_t ld, void* stream);
 
 /*
  * Output tile processed by workgroup `block` of a launch over a

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(dll, name), name
     assert sorted(_lib.EXPORTS) == names
-    assert _lib.abi_version() == 1
+    assert _lib.abi_version() == _lib.ABI_VERSION == 2
 
 
 def test_gemm_rejects_bad_arguments_before_launching():
@@ -51,6 +51,10 @@ def test_gemm_rejects_bad_arguments_before_launching():
     assert call(ptrs=(8, 8, 0)) == _lib.E_ARG  # null c
     assert call(M=0) == 0 and call(N=0) == 0  # empty output: nothing launched
     assert _lib.strerror(_lib.E_ARG).decode().startswith("f16acc")
+    a = args
+    for bad_tile in (-1, len(_lib.TILES), 99):  # forced tile out of range
+        assert _lib.gemm_tile(8, 8, 8, None, a["M"], a["N"], a["K"], a["sam"], a["sak"], a["sbk"], a["sbn"],
+                              a["scm"], a["scn"], 0, 1, None, bad_tile) == _lib.E_ARG
 
 
 def test_block_to_tile_map_is_a_bijection():
@@ -95,17 +99,32 @@ class _Fake:
         return self._ptr
 
 
-@pytest.mark.parametrize("M,N,K,sa,sb,fam,bm", [
-    (4096, 4096, 4096, (4096, 1), (4096, 1), "fast", 256),   # row-major b (NC loader)
-    (4096, 4096, 4096, (4096, 1), (1, 4096), "fast", 256),   # w.t() (KC loader)
-    (2048, 1536, 1536, (1536, 1), (1, 1536), "fast", 128),   # too few 256-tiles to fill the CUs
-    (2049, 1537, 8961, (8961, 1), (1, 8961), "generic", 128),  # rows not 16-byte aligned
-    (300, 200, 256, (512, 2), (700, 3), "generic", 128),      # strided operands
+@pytest.mark.parametrize("M,N,K,sa,sb,fam,tile", [
+    (4096, 4096, 4096, (4096, 1), (4096, 1), "fast", "128x128"),   # row-major b (NC loader); one
+    (4096, 4096, 4096, (4096, 1), (1, 4096), "fast", "128x128"),   # 256-tile per CU loses to 128
+    (8192, 8192, 8192, (8192, 1), (8192, 1), "fast", "256x256"),   # four 256-tiles per CU
+    (2048, 8960, 1536, (1536, 1), (1, 1536), "fast", "128x128"),   # 280 256-tiles: ragged 2nd wave
+    (2048, 1536, 1536, (1536, 1), (1, 1536), "fast", "128x128"),   # too few 256-tiles to fill the CUs
+    (2049, 1537, 8961, (8961, 1), (1, 8961), "generic", "generic"),  # rows not 16-byte aligned
+    (300, 200, 256, (512, 2), (700, 3), "generic", "generic"),      # strided operands
 ])
-def test_tile_table(M, N, K, sa, sb, fam, bm):
+def test_tile_table(M, N, K, sa, sb, fam, tile):
     cfg = tile_config(_Fake((M, K), sa), _Fake((K, N), sb))
-    assert cfg["family"] == fam and cfg["bm"] == bm
+    assert cfg["family"] == fam and cfg["tile"] == tile
     assert cfg["tiles_m"] == -(-M // cfg["bm"]) and cfg["tiles_n"] == -(-N // cfg["bn"])
+
+
+@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic"])
+def test_forced_tile_resolves(tile):
+    bm, bn = (128, 128) if tile == "generic" else map(int, tile.split("x"))
+    cfg = tile_config(_Fake((4096, 1024), (1024, 1)), _Fake((1024, 2048), (2048, 1)), tile)
+    assert cfg["tile"] == tile and (cfg["bm"], cfg["bn"]) == (bm, bn)
+    assert cfg["family"] == ("generic" if tile == "generic" else "fast")
+    # strided operands cannot take a fast tile: the forced choice falls back
+    cfg = tile_config(_Fake((300, 256), (512, 2)), _Fake((256, 200), (700, 3)), tile)
+    assert cfg["tile"] == "generic"
+    with pytest.raises(ValueError):
+        tile_config(_Fake((4096, 1024), (1024, 1)), _Fake((1024, 2048), (2048, 1)), "64x64")
 
 
 def test_misaligned_pointer_takes_the_generic_path():

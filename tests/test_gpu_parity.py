@@ -120,3 +120,109 @@ def test_zero_sizes():
     assert c.shape == (0, 32)
     c = f16acc.mm(rnd((64, 64), 1).cuda(), rnd((64, 0), 2).cuda())
     assert c.shape == (64, 0)
+
+
+@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic"])
+@pytest.mark.parametrize("K", [64, 128, 192, 200, 320, 1024])
+def test_every_tile_matches_oracle(tile, K):
+    """Each tile configuration, forced, on ragged M/N edges, for K of one to
+    sixteen LDS stages (the three-stage rings of 256x128 / 128x256 see every
+    fill and drain case), both B layouts, both output dtypes."""
+    from f16acc_amd.kernel import mm_tile
+
+    M, N = 300, 520
+    a, b = rnd((M, K), 10 + K), rnd((K, N), 11 + K)
+    ga = a.cuda()
+    for b_t in (False, True):
+        gb = b.t().contiguous().cuda().t() if b_t else b.cuda()
+        cfg = tile_config(ga, gb, tile)
+        assert cfg["tile"] == tile
+        for out_dtype in (torch.float32, torch.float16):
+            c, flags = mm_flags(ga, gb, out_dtype, tile=tile)
+            ref, rflags = oracle(a, b, out_dtype, cfg)
+            assert torch.equal(flags.cpu(), rflags)
+            assert rel(c.cpu(), ref) < TOL, (tile, K, b_t, out_dtype)
+        c32 = mm_tile(ga, gb, tile, torch.float32, chunked=False)
+        assert rel(c32.cpu(), (a.float() @ b.float()).double()) < 1e-5
+
+
+@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic"])
+def test_every_tile_redoes_overflowing_tiles(tile):
+    """Overflow closed form (reference tests/test_f16acc.py:91-101) placed in
+    one tile of a larger grid: that tile is flagged and exact, the others not."""
+    M, N, K = 512, 512, 128
+    a = rnd((M, K), 20, 0.5)
+    b = rnd((K, N), 21, 0.5)
+    a[300:310, :] = 100.0
+    b[:, 400:410] = 0.0
+    b[:32, 400:410], b[32:64, 400:410], b[64:96, 400:410], b[96:, 400:410] = 30.0, -30.0, 30.0, -30.0
+    b[127, 400:410] = -29.0
+    ga, gb = a.cuda(), b.cuda()
+    from f16acc_amd.kernel import tile_config as tc
+
+    cfg = tc(ga, gb, tile)
+    c, flags = mm_flags(ga, gb, torch.float32, tile=tile)
+    ref, rflags = oracle(a, b, torch.float32, cfg)
+    assert torch.equal(flags.cpu(), rflags) and int(flags.sum()) >= 1
+    assert torch.all(c[300:310, 400:410].cpu() == 100.0)
+    assert rel(c.cpu(), ref) < TOL
+
+
+def _packed_case(a, b):
+    """The operands mm runs on after packing, and whether both are fast-path."""
+    from f16acc_amd.kernel import _fast_a, _fast_b, _operands
+
+    M, K = a.shape
+    N = b.shape[1]
+    a2, b2, K2 = _operands(a, b, M, N, K)
+    return a2, b2, K2, _fast_a(a2, K2) and _fast_b(b2, K2, N)
+
+
+@pytest.mark.parametrize("case", ["odd_k", "odd_k_wt", "row_major_odd_n", "offset_view", "strided"])
+def test_packed_operands_match_oracle(case):
+    """Operands the fast kernels cannot read directly are packed (zero-padded
+    K) and run on a fast tile; results match the oracle exactly as well."""
+    M, K, N = 257, 1001, 193
+    if case == "odd_k":  # a [M, K] with K % 8 != 0, b row-major
+        a, b = rnd((M, K), 30), rnd((K, N), 31)
+        ga, gb = a.cuda(), b.cuda()
+    elif case == "odd_k_wt":  # b as the w.t() view of an [N, K] weight
+        a, w = rnd((M, K), 32), rnd((N, K), 33)
+        b = w.t()
+        ga, gb = a.cuda(), w.cuda().t()
+    elif case == "row_major_odd_n":  # row-major b with N % 8 != 0: transposing pack
+        K = 1024
+        a, b = rnd((M, K), 34), rnd((K, N), 35)
+        ga, gb = a.cuda(), b.cuda()
+    elif case == "offset_view":  # views starting one element in: misaligned pointers and strides
+        K = 1024
+        abig, bbig = rnd((M, K + 1), 36), rnd((K + 1, N + 7), 37)
+        a, b = abig[:, 1:], bbig[1:, 3:3 + N]
+        ga, gb = abig.cuda()[:, 1:], bbig.cuda()[1:, 3:3 + N]
+    else:  # both operands strided in both dimensions
+        abig, bbig = rnd((M, 2 * K), 38), rnd((K, 3 * N), 39)
+        a, b = abig[:, ::2], bbig[:, 1::3]
+        ga, gb = abig.cuda()[:, ::2], bbig.cuda()[:, 1::3]
+    a2, b2, K2, fast = _packed_case(ga, gb)
+    assert fast and K2 % 8 == 0 and K2 - a.shape[1] < 8
+    cfg = tile_config(a2, b2)
+    for out_dtype in (torch.float32, torch.float16):
+        c, flags = mm_flags(ga, gb, out_dtype)
+        ref, rflags = oracle(a, b, out_dtype, cfg)
+        assert torch.equal(flags.cpu(), rflags)
+        assert rel(c.cpu(), ref) < TOL, (case, out_dtype)
+        assert rel(c.cpu(), a.double() @ b.double()) < 2e-3
+
+
+def test_odd_config_2049_1537_8961():
+    """The odd Qwen-layer config (M=2049, N=1537, K=8961, weight stored
+    [N, K]) against the oracle: K-padding by the pack must not change the
+    last, one-element chunk."""
+    a, w = rnd((2049, 8961), 40), rnd((1537, 8961), 41, 0.02)
+    ga, gw = a.cuda(), w.cuda()
+    c, flags = mm_flags(ga, gw.t(), torch.float32)
+    a2, b2, _, fast = _packed_case(ga, gw.t())
+    assert fast
+    ref, rflags = oracle(a, w.t(), torch.float32, tile_config(a2, b2))
+    assert int(flags.sum()) == 0 and int(rflags.sum()) == 0
+    assert rel(c.cpu(), ref) < TOL
