@@ -15,17 +15,20 @@ import tempfile
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 SRC = os.path.join(PKG, "csrc", "f16acc_gemm.hip")
+CHUNKRATE_SRC = os.path.join(PKG, "csrc", "chunkrate.hip")
 INCLUDE = os.path.join(ROOT, "include")
 OUT_DIR = os.path.join(PKG, "_build")
 LIB = os.path.join(OUT_DIR, "libf16acc_amd.so")
+CHUNKRATE = os.path.join(OUT_DIR, "chunkrate")  # MFMA / chunk-epilogue microbenchmark
 ARCH = "gfx950"
 
 # -packed-fp32-ops: hipcc may otherwise fuse FP32 pairs into v_pk_* ops
-HIP_FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
 ]
+HIP_FLAGS = COMMON_FLAGS + ["-fPIC", "-shared"]
 
 
 def hipcc():
@@ -35,12 +38,12 @@ def hipcc():
     raise FileNotFoundError("hipcc not found (set HIPCC or install ROCm under /opt/rocm)")
 
 
-def build(verbose=False):
-    """Compile the library; the previous .so is replaced atomically."""
+def _compile(flags, src, out, verbose):
+    """hipcc src -> out; the previous output is replaced atomically."""
     os.makedirs(OUT_DIR, exist_ok=True)
-    fd, tmp = tempfile.mkstemp(suffix=".so", dir=OUT_DIR)
+    fd, tmp = tempfile.mkstemp(suffix=".tmp", dir=OUT_DIR)
     os.close(fd)
-    cmd = [hipcc(), *HIP_FLAGS, "-I", INCLUDE, SRC, "-o", tmp]
+    cmd = [hipcc(), *flags, "-I", INCLUDE, src, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         os.unlink(tmp)
@@ -50,8 +53,15 @@ def build(verbose=False):
         msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if not any(n in ln for n in noise)]
         if msgs:
             print("\n".join(msgs), file=sys.stderr)
-    os.replace(tmp, LIB)
-    return LIB
+    os.chmod(tmp, 0o755)
+    os.replace(tmp, out)
+    return out
+
+
+def build(verbose=False):
+    """Compile the library and the chunkrate microbenchmark."""
+    _compile(COMMON_FLAGS, CHUNKRATE_SRC, CHUNKRATE, verbose)
+    return _compile(HIP_FLAGS, SRC, LIB, verbose)
 
 
 if __name__ == "__main__":

@@ -1,0 +1,242 @@
+// chunkrate: what the chunk-32 emulation costs on the MFMA pipe of gfx950.
+//
+// The MI355X counterpart of the reference's bench/rate.py (MMA rate with
+// FP32 vs FP16 accumulation) and bench/chunkrate.py (cost of promoting FP16
+// accumulators to FP32 every few K steps).  gfx950 has no FP16-accumulating
+// MFMA, so the question becomes: how fast can a 16x16x32 chunk MFMA with a
+// zero accumulator be followed by the FP16 rounding of its result and the
+// FP32 sum, compared with plain FP32-accumulating MFMAs?
+//
+// Register-only loops (no memory traffic), every instruction in inline asm so
+// the issue order is exactly the program order.  Each measurement reports
+// shader-clock cycles (s_memtime) per "block step" per SIMD: two chunk MFMAs
+// of one 16x16 output block (ideal 32 cycles) plus whatever the variant adds.
+//
+//   part 1  which VALU instruction classes overlap an MFMA: per step one MFMA
+//           then four VALU ops of one class (16 cycles if fully hidden)
+//   part 2  complete chunk epilogues, software pipelined (the epilogue of
+//           block j-2 runs next to the MFMAs of block j)
+//
+//   usage: chunkrate            (needs one gfx950 GPU; prints a table)
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+
+namespace {
+
+typedef _Float16 f16;
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+#define CHECK(x)                                                                   \
+  do {                                                                             \
+    hipError_t e_ = (x);                                                           \
+    if (e_ != hipSuccess) {                                                        \
+      std::fprintf(stderr, "HIP error %s at line %d\n", hipGetErrorString(e_), __LINE__); \
+      std::exit(1);                                                                \
+    }                                                                              \
+  } while (0)
+
+constexpr int kIters = 20000;
+constexpr int kThreads = 256;
+
+// ---- part 1: MFMA + four VALU ops of one class -----------------------------
+#define MFMA_ACC(acc, a, b) asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b))
+
+template <int T>
+__device__ __forceinline__ void valu4(float& x0, float& x1, float& x2, float& x3, unsigned& h0, unsigned& h1) {
+#define V4(s) asm volatile(s : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3), "+v"(h0), "+v"(h1))
+  if (T == 0) V4("v_add_f32 %0, %0, %1\n v_add_f32 %1, %1, %2\n v_add_f32 %2, %2, %3\n v_add_f32 %3, %3, %0");
+  if (T == 1) V4("v_cvt_pk_f16_f32 %4, %0, %1\n v_cvt_pk_f16_f32 %5, %2, %3\n v_cvt_pk_f16_f32 %4, %1, %2\n v_cvt_pk_f16_f32 %5, %3, %0");
+  if (T == 2) V4("v_dot2c_f32_f16 %0, %4, %5\n v_dot2c_f32_f16 %1, %5, %4\n v_dot2c_f32_f16 %2, %4, %5\n v_dot2c_f32_f16 %3, %5, %4");
+  if (T == 3) V4("v_fma_mix_f32 %0, %4, %5, %0 op_sel_hi:[1,1,0]\n v_fma_mix_f32 %1, %4, %5, %1 op_sel_hi:[1,1,0]\n v_fma_mix_f32 %2, %4, %5, %2 op_sel_hi:[1,1,0]\n v_fma_mix_f32 %3, %4, %5, %3 op_sel_hi:[1,1,0]");
+  if (T == 4) V4("v_add_u32 %4, %4, %5\n v_add_u32 %5, %5, %4\n v_xor_b32 %4, %4, %5\n v_add_u32 %5, %5, %4");
+  if (T == 5) V4("v_pk_add_f16 %4, %4, %5\n v_pk_add_f16 %5, %5, %4\n v_pk_add_f16 %4, %4, %5\n v_pk_add_f16 %5, %5, %4");
+  if (T == 6) V4("v_cvt_f32_f16 %0, %4\n v_cvt_f32_f16 %1, %5\n v_cvt_f32_f16 %2, %4\n v_cvt_f32_f16 %3, %5");
+  if (T == 7) V4("v_fma_f32 %0, %0, %1, %2\n v_fma_f32 %1, %1, %2, %3\n v_fma_f32 %2, %2, %3, %0\n v_fma_f32 %3, %3, %0, %1");
+#undef V4
+}
+constexpr const char* kValuNames[] = {"v_add_f32", "v_cvt_pk_f16_f32", "v_dot2c_f32_f16", "v_fma_mix_f32",
+                                      "v_add_u32 / v_xor_b32", "v_pk_add_f16", "v_cvt_f32_f16", "v_fma_f32"};
+
+// MODE 0: MFMA + VALU interleaved, 1: MFMA only, 2: VALU only
+template <int T, int MODE>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void overlap_kernel(
+    float* out, int iters, unsigned long long* cyc) {
+  const int lane = threadIdx.x & 63;
+  f16x8 a0, a1;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    a0[e] = (f16)(0.01f * (lane + e));
+    a1[e] = (f16)(0.02f * (lane - e));
+  }
+  f32x4 acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, (float)j};
+  float x0 = lane, x1 = 1.f, x2 = 2.f, x3 = 3.f;
+  unsigned h0 = 0x3c003c00u + lane, h1 = 0x3c003c00u;
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if (MODE != 2) MFMA_ACC(acc[j], a0, a1);
+      if (MODE != 1) valu4<T>(x0, x1, x2, x3, h0, h1);
+    }
+  }
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  float s = x0 + x1 + x2 + x3 + (float)(h0 ^ h1);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) s += acc[j][0] + acc[j][3];
+  out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+  if (threadIdx.x == 0) cyc[blockIdx.x] = t1 - t0;
+}
+
+// ---- part 2: complete chunk epilogues ----------------------------------------
+#define MFMA_ZERO(d, a, b) asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b))
+#define CVT_PK(h, x, y) asm volatile("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(h) : "v"(x), "v"(y))
+#define MIX_LO(s, h) asm volatile("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel_hi:[1,0,0]" : "+v"(s) : "v"(h))
+#define MIX_HI(s, h) asm volatile("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(s) : "v"(h))
+#define DOT2(s, h) asm volatile("v_dot2c_f32_f16 %0, %1, %2" : "+v"(s) : "v"(h), "v"(ones))
+
+// E: 0 FP32-accumulating MFMAs (the reference's chunked=False), 1 cvt_pk + dot2,
+//    2 cvt_pk + fma_mix, 3 cvt_pk + selector MFMA (the shipped epilogue),
+//    4 cvt_pk alone (no sum: a lower bound)
+template <int E>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void epilogue_kernel(
+    float* out, int iters, unsigned long long* cyc) {
+  constexpr int NB = 8;
+  const int lane = threadIdx.x & 63;
+  f16x8 a0, a1, b[NB], sel;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    a0[e] = (f16)(0.01f * (lane + e));
+    a1[e] = (f16)(0.02f * (lane - e));
+    sel[e] = (4 * (lane >> 4) + (e >> 1) == (lane & 15)) ? (f16)1.0f : (f16)0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) b[j][e] = (f16)(0.001f * (lane * (j + 1) + e));
+  const unsigned ones = 0x3c003c00u;
+  f32x4 p0[NB], p1[NB], S[NB];
+  u32x4 h[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    p0[j] = p1[j] = S[j] = f32x4{0.f, 0.f, 0.f, (float)j};
+    h[j] = u32x4{0u, 0u, 0u, 0u};
+  }
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int q = (j + NB - 2) % NB;  // block whose epilogue runs now: its MFMAs are 4 MFMAs old
+      if (E == 0) {
+        MFMA_ACC(S[j], b[j], a0);
+        MFMA_ACC(S[j], b[j], a1);
+        continue;
+      }
+      MFMA_ZERO(p0[j], b[j], a0);
+      if (E == 3) {
+        CVT_PK(h[q][0], p0[q][0], p1[q][0]);
+        CVT_PK(h[q][1], p0[q][1], p1[q][1]);
+      } else {
+        CVT_PK(h[q][0], p0[q][0], p1[q][0]);
+        CVT_PK(h[q][1], p0[q][1], p1[q][1]);
+        CVT_PK(h[q][2], p0[q][2], p1[q][2]);
+        CVT_PK(h[q][3], p0[q][3], p1[q][3]);
+      }
+      MFMA_ZERO(p1[j], b[j], a1);
+      if (E == 1) {
+        DOT2(S[q][0], h[q][0]); DOT2(S[q][1], h[q][1]); DOT2(S[q][2], h[q][2]); DOT2(S[q][3], h[q][3]);
+      } else if (E == 2) {
+        MIX_LO(S[q][0], h[q][0]); MIX_HI(S[q][0], h[q][0]); MIX_LO(S[q][1], h[q][1]); MIX_HI(S[q][1], h[q][1]);
+        MIX_LO(S[q][2], h[q][2]); MIX_HI(S[q][2], h[q][2]); MIX_LO(S[q][3], h[q][3]); MIX_HI(S[q][3], h[q][3]);
+      } else if (E == 3) {
+        CVT_PK(h[q][2], p0[q][2], p1[q][2]);
+        CVT_PK(h[q][3], p0[q][3], p1[q][3]);
+        const int r = (j + NB - 3) % NB;  // rounded during the previous step
+        MFMA_ACC(S[r], sel, h[r]);
+      }
+    }
+  }
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NB; ++j) s += S[j][0] + S[j][3] + p0[j][1] + p1[j][2] + (float)h[j][1];
+  out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+  if (threadIdx.x == 0) cyc[blockIdx.x] = t1 - t0;
+}
+
+struct Bufs {
+  float* out = nullptr;
+  unsigned long long* cyc = nullptr;
+  int blocks = 0;
+};
+
+// Cycles per inner step per SIMD: the slowest workgroup's s_memtime span over
+// its iterations, divided by the steps its SIMD ran (waves_per_simd waves).
+template <class K>
+double measure(K kernel, const Bufs& b, int steps_per_iter, int waves_per_simd) {
+  hipLaunchKernelGGL(kernel, dim3(b.blocks), dim3(kThreads), 0, 0, b.out, 10, b.cyc);  // warm-up
+  CHECK(hipDeviceSynchronize());
+  hipLaunchKernelGGL(kernel, dim3(b.blocks), dim3(kThreads), 0, 0, b.out, kIters, b.cyc);
+  CHECK(hipDeviceSynchronize());
+  std::vector<unsigned long long> c(b.blocks);
+  CHECK(hipMemcpy(c.data(), b.cyc, c.size() * sizeof(c[0]), hipMemcpyDeviceToHost));
+  unsigned long long mx = 0;
+  for (auto x : c) mx = x > mx ? x : mx;
+  return (double)mx / ((double)kIters * steps_per_iter * waves_per_simd);
+}
+
+template <int T>
+void part1_row(const Bufs& b, int w) {
+  const double both = measure(overlap_kernel<T, 0>, b, 16, w);
+  const double valu = measure(overlap_kernel<T, 2>, b, 16, w);
+  std::printf("  %-22s %8.2f %12.2f\n", kValuNames[T], both, valu);
+}
+
+}  // namespace
+
+int main() {
+  int cus = 0;
+  CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0));
+  hipDeviceProp_t prop;
+  CHECK(hipGetDeviceProperties(&prop, 0));
+  std::printf("chunkrate on %s (%s), %d CUs; cycles are shader clocks (s_memtime) per SIMD\n", prop.name,
+              prop.gcnArchName, cus);
+  for (int w = 1; w <= 2; ++w) {
+    Bufs b;
+    b.blocks = cus * w;  // 4 waves per workgroup: w waves per SIMD
+    CHECK(hipMalloc(&b.out, (size_t)b.blocks * kThreads * sizeof(float)));
+    CHECK(hipMalloc(&b.cyc, (size_t)b.blocks * sizeof(unsigned long long)));
+    std::printf("\n== %d wave(s) per SIMD\n", w);
+    std::printf("part 1: one MFMA 16x16x32 (16 cycles) + four VALU ops; cycles per step\n");
+    std::printf("  %-22s %8s %12s\n", "VALU op", "MFMA+4op", "4 ops alone");
+    std::printf("  %-22s %8.2f\n", "(MFMA alone)", measure(overlap_kernel<0, 1>, b, 16, w));
+    part1_row<0>(b, w);
+    part1_row<1>(b, w);
+    part1_row<2>(b, w);
+    part1_row<3>(b, w);
+    part1_row<4>(b, w);
+    part1_row<5>(b, w);
+    part1_row<6>(b, w);
+    part1_row<7>(b, w);
+    std::printf("part 2: chunk-pair epilogues; cycles per block step (2 chunk MFMAs = 32 ideal), fraction of peak\n");
+    const char* names[] = {"FP32-accumulating MFMAs", "cvt_pk x4 + dot2 x4", "cvt_pk x4 + fma_mix x8",
+                           "cvt_pk x4 + selector MFMA", "cvt_pk x4 alone (bound)"};
+    double c[5];
+    c[0] = measure(epilogue_kernel<0>, b, 8, w);
+    c[1] = measure(epilogue_kernel<1>, b, 8, w);
+    c[2] = measure(epilogue_kernel<2>, b, 8, w);
+    c[3] = measure(epilogue_kernel<3>, b, 8, w);
+    c[4] = measure(epilogue_kernel<4>, b, 8, w);
+    for (int i = 0; i < 5; ++i) std::printf("  %-28s %8.2f  %.3f\n", names[i], c[i], 32.0 / c[i]);
+    CHECK(hipFree(b.out));
+    CHECK(hipFree(b.cyc));
+  }
+  return 0;
+}
