@@ -159,6 +159,64 @@ def sweep_tiles(names):
         torch.cuda.empty_cache()
 
 
+def overflow_inputs(n=4096, blocks=7, block=128, seed=0):
+    """Overflow stress GEMM: a, b ~ N(0, 1) fp16 (b row-major [K, N]) with
+    `blocks` of the n/block row-blocks of a and column-blocks of b set to
+    U(200, 255), chosen from the seed.  Their intersection tiles (7 x 7 of
+    32 x 32 = 4.8 % of 128 x 128 tiles) have 32-term chunk sums near
+    32 * 227^2 = 1.65e6 > 65504, inf in fp16, so they are flagged and redone
+    in FP32; row-only or column-only blocks stay near 1.3e3."""
+    g = torch.Generator().manual_seed(seed)
+    a = torch.randn(n, n, generator=g)
+    b = torch.randn(n, n, generator=g)
+    nb = n // block
+    rows = torch.randperm(nb, generator=g)[:blocks].tolist()
+    cols = torch.randperm(nb, generator=g)[:blocks].tolist()
+    for r in rows:
+        a[r * block:(r + 1) * block] = 200.0 + 55.0 * torch.rand(block, n, generator=g)
+    for c in cols:
+        b[:, c * block:(c + 1) * block] = 200.0 + 55.0 * torch.rand(n, block, generator=g)
+    return a.half(), b.half(), sorted(rows), sorted(cols)
+
+
+def overflow_bench(steps, warmup):
+    """Overflow stress workload: chunked time with ~5 % of tiles redone in
+    FP32, the same call on the no-overflow data, flagged tiles, and the check
+    that every redone tile equals the FP32-accumulate mode bit for bit."""
+    import f16acc_amd
+    from f16acc_amd.kernel import mm_flags, tile_config
+
+    a_cpu, b_cpu, rows, cols = overflow_inputs()
+    a, b = a_cpu.cuda(), b_cpu.cuda()
+    M, K = a.shape
+    N = b.shape[1]
+    flops = 2.0 * M * N * K
+    cfg = tile_config(a, b)
+    _, ev = time_steps(lambda: f16acc_amd.mm(a, b, torch.float32), steps, warmup)
+    t_over = ev / steps
+    c, flags = mm_flags(a, b, torch.float32)
+    c32 = f16acc_amd.mm(a, b, torch.float32, chunked=False)
+    _, _, ca, cb = make_inputs(M, N, K, "row")
+    _, ev = time_steps(lambda: f16acc_amd.mm(ca, cb, torch.float32), steps, warmup)
+    t_clean = ev / steps
+    bm, bn = cfg["bm"], cfg["bn"]
+    fl = flags.cpu().bool()
+    mask = fl.repeat_interleave(bm, 0).repeat_interleave(bn, 1)[:M, :N].cuda()
+    redone_exact = bool(torch.equal(c[mask], c32[mask]))
+    ref = a.double() @ b.double()
+    keep = ~mask
+    err_other = ((c.double() - ref).abs()[keep].max() / ref.abs()[keep].max()).item()
+    line = {"workload": "overflow stress 4096^3, fp32 out, B row-major", "tile": cfg["tile"],
+            "tiles": cfg["tiles_m"] * cfg["tiles_n"], "flagged_tiles": int(fl.sum()),
+            "expected_flagged": "the 7x7 block intersections at 128x128 tiles",
+            "us_with_overflow": round(t_over * 1e6, 2), "us_without_overflow": round(t_clean * 1e6, 2),
+            "tflops_with_overflow": round(flops / t_over / 1e12, 1),
+            "tflops_without_overflow": round(flops / t_clean / 1e12, 1),
+            "redone_tiles_equal_fp32_mode": redone_exact, "max_rel_err_other_tiles_vs_fp64": err_other,
+            "rows": rows, "cols": cols}
+    print(json.dumps(line), flush=True)
+
+
 def copy_reference(steps, warmup, nbytes=1 << 30):
     """A plain device copy of known size (1 GiB read + 1 GiB written per step):
     the calibration for rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
@@ -174,18 +232,21 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="gemm4096", choices=sorted(WORKLOADS) + ["copy"])
+    ap.add_argument("--workload", default="gemm4096", choices=sorted(WORKLOADS) + ["copy", "overflow"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and oracle comparison")
     ap.add_argument("--sweep-tiles", nargs="*", metavar="WORKLOAD",
                     help="time every tile configuration on these workloads (all if none given) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (a GEMM shards by M or N "
-              "tiles with no exchange, see DESIGN.md); run it with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: there is no multi-GPU path (a GEMM would shard by M or N "
+              "tiles with no exchange, or by K in multiples of 32 with one FP32 all-reduce); "
+              "run it with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     if args.workload == "copy":
         return copy_reference(args.steps, args.warmup)
+    if args.workload == "overflow":
+        return overflow_bench(args.steps, args.warmup)
     if args.sweep_tiles is not None:
         return sweep_tiles(args.sweep_tiles or sorted(WORKLOADS))
 

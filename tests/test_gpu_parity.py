@@ -226,3 +226,26 @@ def test_odd_config_2049_1537_8961():
     ref, rflags = oracle(a, w.t(), torch.float32, tile_config(a2, b2))
     assert int(flags.sum()) == 0 and int(rflags.sum()) == 0
     assert rel(c.cpu(), ref) < TOL
+
+
+def test_overflow_stress_flags_exactly_the_block_intersections():
+    """The overflow stress workload at 1024^2 x 1024 with 2 of 8 row-blocks of
+    a and column-blocks of b set to U(200, 255): only the 4 intersection tiles
+    overflow; they are flagged like the oracle's, equal the FP32-accumulate
+    mode bit for bit (same tile, same summation order), and every other tile
+    matches the oracle."""
+    import bench
+
+    a, b, rows, cols = bench.overflow_inputs(n=1024, blocks=2)
+    ga, gb = a.cuda(), b.cuda()
+    cfg = tile_config(ga, gb)
+    c, flags = mm_flags(ga, gb, torch.float32)
+    c32 = f16acc.mm(ga, gb, torch.float32, chunked=False)
+    ref, rflags = oracle(a, b, torch.float32, cfg)
+    assert torch.equal(flags.cpu(), rflags)
+    bm, bn = cfg["bm"], cfg["bn"]
+    want = {(r * 128 // bm, q * 128 // bn) for r in rows for q in cols}
+    assert {tuple(t) for t in flags.nonzero().tolist()} == want
+    mask = flags.bool().repeat_interleave(bm, 0).repeat_interleave(bn, 1)[:1024, :1024]
+    assert torch.equal(c[mask], c32[mask])
+    assert rel(c.cpu()[~mask.cpu()], ref[~mask.cpu()]) < TOL
