@@ -48,6 +48,7 @@ WORKLOADS = {
     "qwen_gateup": (2048, 8960, 1536, "t", torch.float16),
     "qwen_down": (2048, 1536, 8960, "t", torch.float16),
     "odd": (2049, 1537, 8961, "t", torch.float16),
+    "qwen_lm_head": (2048, 151936, 1536, "t", torch.float16),
 }
 
 
@@ -217,6 +218,83 @@ def overflow_bench(steps, warmup):
     print(json.dumps(line), flush=True)
 
 
+def qwen2_model(layers=28, seed=0, dtype=torch.float16):
+    """Random-init Qwen2.5-1.5B architecture on the GPU: hidden 1536, SwiGLU
+    8960, 12 query / 2 KV heads (head_dim 128), RMSNorm eps 1e-6, RoPE theta
+    1e6, vocab 151936, tied embeddings, weights N(0, 0.02) (the library's
+    initializer; biases start at 0).  No checkpoint is read."""
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    cfg = Qwen2Config(hidden_size=1536, intermediate_size=8960, num_hidden_layers=layers, num_attention_heads=12,
+                      num_key_value_heads=2, rms_norm_eps=1e-6,
+                      rope_parameters={"rope_type": "default", "rope_theta": 1e6}, vocab_size=151936,
+                      tie_word_embeddings=True, initializer_range=0.02, max_position_embeddings=32768)
+    torch.manual_seed(seed)
+    with torch.device("cuda"):
+        model = Qwen2ForCausalLM(cfg)
+    return model.to(dtype).eval()
+
+
+def qwen2_prefill_ab(layers=28, tokens=2048, seed=0, reps=5):
+    """Prefill A/B on the random-init model, batch 1, seeded random tokens:
+    logits of the unpatched FP16 model (hipBLASLt) and of the patched one
+    (every nn.Linear through f16acc_amd.mm), each against an FP32 run of the
+    same weights.  Returns top-1 agreement, mean next-token cross-entropy and
+    prefill time; the analogue of the reference's bench/llm.py:33-64 without
+    the checkpoint download."""
+    import torch.nn.functional as F
+
+    import f16acc_amd
+    from f16acc_amd import patch
+
+    ids = torch.randint(0, 151936, (1, tokens), generator=torch.Generator().manual_seed(seed)).cuda()
+    model = qwen2_model(layers, seed, torch.float32)
+
+    def run():
+        with torch.no_grad():
+            return model(ids).logits[0].float()
+
+    def timed():
+        ts = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            run()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    ref = run()
+    model.half()
+    base = run()
+    t_base = timed()
+    for k in patch.calls:
+        patch.calls[k] = 0
+    f16acc_amd.enable()
+    try:
+        ours = run()
+        n_calls = dict(patch.calls)
+        t_ours = timed()
+    finally:
+        f16acc_amd.disable()
+    tgt = ids[0, 1:]
+
+    def ce(lg):
+        return F.cross_entropy(lg[:-1], tgt).item()
+
+    top = {n: lg.argmax(-1) for n, lg in (("ref", ref), ("base", base), ("ours", ours))}
+    return {"layers": layers, "tokens": tokens,
+            "top1_patched_vs_unpatched": (top["ours"] == top["base"]).float().mean().item(),
+            "top1_unpatched_vs_fp32": (top["base"] == top["ref"]).float().mean().item(),
+            "top1_patched_vs_fp32": (top["ours"] == top["ref"]).float().mean().item(),
+            "mean_ce_fp32": ce(ref), "mean_ce_unpatched": ce(base), "mean_ce_patched": ce(ours),
+            "max_abs_logit_diff_patched_vs_fp32": (ours - ref).abs().max().item(),
+            "max_abs_logit_diff_unpatched_vs_fp32": (base - ref).abs().max().item(),
+            "calls_in_one_forward": n_calls,
+            "prefill_ms_unpatched": round(t_base * 1e3, 2), "prefill_ms_patched": round(t_ours * 1e3, 2),
+            "tokens_per_s_unpatched": round(tokens / t_base, 1), "tokens_per_s_patched": round(tokens / t_ours, 1)}
+
+
 def copy_reference(steps, warmup, nbytes=1 << 30):
     """A plain device copy of known size (1 GiB read + 1 GiB written per step):
     the calibration for rocprofv3's FETCH_SIZE / WRITE_SIZE counters."""
@@ -232,7 +310,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="gemm4096", choices=sorted(WORKLOADS) + ["copy", "overflow"])
+    ap.add_argument("--workload", default="gemm4096", choices=sorted(WORKLOADS) + ["copy", "overflow", "qwen2_prefill"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and oracle comparison")
     ap.add_argument("--sweep-tiles", nargs="*", metavar="WORKLOAD",
                     help="time every tile configuration on these workloads (all if none given) and exit")
@@ -247,6 +325,10 @@ def main():
         return copy_reference(args.steps, args.warmup)
     if args.workload == "overflow":
         return overflow_bench(args.steps, args.warmup)
+    if args.workload == "qwen2_prefill":
+        line = {"workload": "random-init Qwen2.5-1.5B FP16 prefill, batch 1, 2048 seeded tokens",
+                **qwen2_prefill_ab()}
+        return print(json.dumps(line), flush=True)
     if args.sweep_tiles is not None:
         return sweep_tiles(args.sweep_tiles or sorted(WORKLOADS))
 
