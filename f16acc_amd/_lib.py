@@ -22,6 +22,10 @@ gemm = _dll.f16acc_gemm
 gemm.argtypes = [_vp, _vp, _vp, _vp] + [_i64] * 9 + [_int, _int, _vp]
 gemm.restype = _int
 
+gemm_bias = _dll.f16acc_gemm_bias
+gemm_bias.argtypes = [_vp, _vp, _vp, _vp, _vp] + [_i64] * 9 + [_int, _int, _vp]
+gemm_bias.restype = _int
+
 gemm_tile = _dll.f16acc_gemm_tile
 gemm_tile.argtypes = [_vp, _vp, _vp, _vp] + [_i64] * 9 + [_int, _int, _vp, _int]
 gemm_tile.restype = _int
@@ -47,7 +51,7 @@ abi_version.argtypes = []
 abi_version.restype = _int
 
 # Exported symbol names, as declared in include/f16acc.h.
-EXPORTS = ("f16acc_gemm", "f16acc_gemm_tile", "f16acc_pack", "f16acc_tile_config", "f16acc_block_tile", "f16acc_strerror",
+EXPORTS = ("f16acc_gemm", "f16acc_gemm_bias", "f16acc_gemm_tile", "f16acc_pack", "f16acc_tile_config", "f16acc_block_tile", "f16acc_strerror",
            "f16acc_abi_version")
 ABI_VERSION = 2
 

@@ -67,6 +67,7 @@ struct Params {
   const f16* b;
   void* c;
   uint8_t* flags;
+  const f16* bias;  // optional [N] vector added in the epilogue (NULL: none)
   int64_t M, N, K;
   int64_t sam, sak, sbk, sbn, scm, scn;
   int64_t tiles_m, tiles_n;
@@ -415,6 +416,18 @@ __device__ __forceinline__ void k_loop_generic(const Params& p, int64_t m0, int6
   }
 }
 
+// Output value of one element.  With a bias the epilogue reproduces the
+// reference's unfused sequence (f16acc/patch.py:28-30: y = mm(...) in fp16,
+// then y += b, which torch evaluates as fp16(float(y) + float(b))): the FP32
+// sum is rounded to binary16 first, the bias is added in FP32 and the result
+// rounded again.  An FP32 output adds the bias to the FP32 sum directly.
+template <bool OUT32>
+__device__ __forceinline__ float with_bias(float v, const f16* bias, int64_t col) {
+  if (!bias) return v;
+  const float b = (float)bias[col];
+  return OUT32 ? v + b : (float)(f16)v + b;
+}
+
 template <class C, bool OUT32>
 __device__ __forceinline__ void store_tile(const Params& p, int64_t m0, int64_t n0, int wm, int wn, int lane,
                                            const f32x4 (&acc)[C::FM][C::FN]) {
@@ -426,8 +439,12 @@ __device__ __forceinline__ void store_tile(const Params& p, int64_t m0, int64_t 
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) {
       const int64_t col = n0 + wn * C::WTN + 16 * j + 4 * g;
-      const f32x4 v = acc[i][j];
+      f32x4 v = acc[i][j];
       if (p.vec_store && col + 3 < p.N) {
+        if (p.bias) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = with_bias<OUT32>(v[r], p.bias, col + r);
+        }
         if (OUT32) {
           *(f32x4*)((float*)p.c + row * p.scm + col) = v;
         } else {
@@ -442,10 +459,11 @@ __device__ __forceinline__ void store_tile(const Params& p, int64_t m0, int64_t 
         for (int r = 0; r < 4; ++r) {
           if (col + r >= p.N) break;
           const int64_t off = row * p.scm + (col + r) * p.scn;
+          const float o = with_bias<OUT32>(v[r], p.bias, col + r);
           if (OUT32)
-            ((float*)p.c)[off] = v[r];
+            ((float*)p.c)[off] = o;
           else
-            ((f16*)p.c)[off] = (f16)v[r];
+            ((f16*)p.c)[off] = (f16)o;
         }
       }
     }
@@ -657,8 +675,8 @@ hipError_t launch_fast(const Params& p, int blayout, int out32, int chunked, hip
                         : launch_cfg<CF<kNC>, true>(p, out32, chunked, st);
 }
 
-int gemm_impl(const void* a, const void* b, void* c, uint8_t* tile_flags, int64_t M, int64_t N, int64_t K,
-              int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int out_dtype,
+int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* tile_flags, int64_t M, int64_t N,
+              int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int out_dtype,
               int chunked, void* stream, int forced_tile) {
   if (M < 0 || N < 0 || K < 0) return F16ACC_E_ARG;
   if (out_dtype != F16ACC_OUT_F16 && out_dtype != F16ACC_OUT_F32) return F16ACC_E_ARG;
@@ -672,6 +690,7 @@ int gemm_impl(const void* a, const void* b, void* c, uint8_t* tile_flags, int64_
   p.b = (const f16*)b;
   p.c = c;
   p.flags = tile_flags;
+  p.bias = (const f16*)bias;
   p.M = M; p.N = N; p.K = K;
   p.sam = sam; p.sak = sak; p.sbk = sbk; p.sbn = sbn; p.scm = scm; p.scn = scn;
   p.tiles_m = cdiv(M, kTiles[ch.tile].bm);
@@ -730,7 +749,16 @@ int f16acc_tile_config(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak
 int f16acc_gemm(const void* a, const void* b, void* c, uint8_t* tile_flags, int64_t M, int64_t N, int64_t K,
                 int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int out_dtype,
                 int chunked, void* stream) {
-  return gemm_impl(a, b, c, tile_flags, M, N, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked, stream, -1);
+  return gemm_impl(a, b, nullptr, c, tile_flags, M, N, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked, stream,
+                   -1);
+}
+
+int f16acc_gemm_bias(const void* a, const void* b, const void* bias, void* c, uint8_t* tile_flags, int64_t M,
+                     int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int64_t scm,
+                     int64_t scn, int out_dtype, int chunked, void* stream) {
+  if (!bias && M > 0 && N > 0) return F16ACC_E_ARG;
+  return gemm_impl(a, b, bias, c, tile_flags, M, N, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked, stream,
+                   -1);
 }
 
 int f16acc_pack(const void* src, void* dst, int64_t rows, int64_t cols, int64_t s_r, int64_t s_c,
@@ -755,7 +783,8 @@ int f16acc_gemm_tile(const void* a, const void* b, void* c, uint8_t* tile_flags,
                      int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int out_dtype,
                      int chunked, void* stream, int tile) {
   if (tile < 0) return F16ACC_E_ARG;
-  return gemm_impl(a, b, c, tile_flags, M, N, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked, stream, tile);
+  return gemm_impl(a, b, nullptr, c, tile_flags, M, N, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked, stream,
+                   tile);
 }
 
 }  // extern "C"

@@ -54,6 +54,27 @@ def mm(a, b, out_dtype=torch.float16, chunked=True):
     return c
 
 
+def mm_bias(a, b, bias, out_dtype=torch.float16, chunked=True):
+    """mm(a, b) + bias with the add fused into the GEMM's store (f16acc_gemm_bias).
+
+    bias: fp16 [N] on a's device.  For an fp16 output the result equals the
+    reference's unfused `y = mm(a, b); y += bias` (f16acc/patch.py:28-30) bit
+    for bit: the FP32 sum is rounded to fp16, the bias added in FP32 and the
+    sum rounded again, as torch's fp16 add does."""
+    _validate(a, b, out_dtype)
+    N = b.shape[1]
+    if (bias.dim() != 1 or bias.shape[0] != N or bias.dtype != torch.float16 or not bias.is_cuda
+            or bias.device != a.device):
+        raise ValueError(f"mm_bias needs an fp16 [{N}] bias on {a.device}, got {tuple(bias.shape)} {bias.dtype}")
+    M, K = a.shape
+    c = torch.empty(M, N, device=a.device, dtype=out_dtype)
+    if M == 0 or N == 0:
+        return c
+    a, b, K = _operands(a, b, M, N, K)
+    _launch(a, b, c, None, M, N, K, chunked, bias=bias.contiguous())
+    return c
+
+
 def _fast_a(a, K):
     """a [M, K] as the fast kernels read it: K-contiguous 16-byte aligned rows."""
     return K % 8 == 0 and (a.stride(1) == 1 or K <= 1) and a.stride(0) % 8 == 0 and a.data_ptr() % 16 == 0
@@ -152,14 +173,19 @@ def tile_config(a, b, tile=None):
             "tiles_n": tn.value, "family": ("fast", "generic")[fam.value], "threads": thr.value}
 
 
-def _launch(a, b, c, flags, M, N, K, chunked, tile=-1):
+def _launch(a, b, c, flags, M, N, K, chunked, tile=-1, bias=None):
     dev = a.device
     if torch.cuda.current_device() != dev.index:
         with torch.cuda.device(dev):
-            return _launch(a, b, c, flags, M, N, K, chunked, tile)
+            return _launch(a, b, c, flags, M, N, K, chunked, tile, bias)
     stream = torch.cuda.current_stream(dev).cuda_stream
-    args = (a.data_ptr(), b.data_ptr(), c.data_ptr(), flags.data_ptr() if flags is not None else None,
-            M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1),
+    ptrs = (a.data_ptr(), b.data_ptr(), c.data_ptr(), flags.data_ptr() if flags is not None else None)
+    args = (M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1),
             _OUT[c.dtype], int(bool(chunked)), stream)
-    rc = _lib.gemm(*args) if tile < 0 else _lib.gemm_tile(*args, tile)
+    if bias is not None:
+        rc = _lib.gemm_bias(ptrs[0], ptrs[1], bias.data_ptr(), ptrs[2], ptrs[3], *args)
+    elif tile < 0:
+        rc = _lib.gemm(*ptrs, *args)
+    else:
+        rc = _lib.gemm_tile(*ptrs, *args, tile)
     _lib.check(rc)

@@ -8,14 +8,16 @@ the module attribute).  Calls whose input is not fp16 on a GPU, whose weight
 is not fp16, that run with gradients enabled, or that have fewer than
 MIN_ROWS rows (decode steps: memory-bound) go to the original F.linear and
 are counted under calls["original"]; the rest go through mm and are counted
-under calls["chunked"].  Overflow is repaired inside the kernel, so there is
-no host sync per call.
+under calls["chunked"].  An fp16 bias is added in the GEMM's store with the
+rounding of the reference's separate `y += b` (patch.py:29-30), so results are
+the same bit for bit.  Overflow is repaired inside the kernel, so there is no
+host sync per call.
 """
 
 import torch
 import torch.nn.functional as F
 
-from .kernel import mm
+from .kernel import mm, mm_bias
 
 MIN_ROWS = 128
 _orig = F.linear
@@ -30,9 +32,15 @@ def linear(x, w, b=None):
     if not eligible:
         calls["original"] += 1
         return _orig(x, w, b)
-    y = mm(x.reshape(rows, x.shape[-1]), w.t())  # w.t() is a (1, K)-strided view; mm takes any strides
-    if b is not None:
-        y += b
+    x2 = x.reshape(rows, x.shape[-1])
+    if (b is not None and b.dtype == torch.float16 and b.dim() == 1 and b.shape[0] == w.shape[0] and b.is_cuda
+            and b.device == x.device):
+        # bias fused into the GEMM's store, rounded as the unfused y += b would be
+        y = mm_bias(x2, w.t(), b)
+    else:
+        y = mm(x2, w.t())  # w.t() is a (1, K)-strided view; mm takes any strides
+        if b is not None:
+            y += b
     calls["chunked"] += 1
     return y.view(*x.shape[:-1], w.shape[0])
 

@@ -74,6 +74,21 @@ int f16acc_gemm(const void* a, const void* b, void* c, uint8_t* tile_flags,
                 int out_dtype, int chunked, void* stream);
 
 /*
+ * f16acc_gemm plus a bias: c[i][j] = a[i] . b[:, j] + bias[j], bias a
+ * contiguous binary16 [N] vector (non-NULL).  Replaces the reference's
+ * nn.Linear routing, f16acc/patch.py:28-30 (y = mm(x2, w.t()); y += b), with
+ * the add fused into the GEMM's store and the same rounding: for a binary16
+ * output the FP32 sum is rounded to binary16, the bias added in FP32 and the
+ * result rounded again (torch's fp16 y += b), so results equal the unfused
+ * sequence bit for bit.  A binary32 output adds the bias to the FP32 sum.
+ */
+int f16acc_gemm_bias(const void* a, const void* b, const void* bias, void* c, uint8_t* tile_flags,
+                     int64_t M, int64_t N, int64_t K,
+                     int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                     int64_t scm, int64_t scn,
+                     int out_dtype, int chunked, void* stream);
+
+/*
  * The tile configuration f16acc_gemm picks for a problem: replaces the
  * reference's autotuned CONFIGS table and best_config handoff
  * (f16acc/kernel.py:16-19, 63, 101-102) with a fixed per-shape table.

@@ -52,6 +52,8 @@ def test_gemm_rejects_bad_arguments_before_launching():
     assert call(M=0) == 0 and call(N=0) == 0  # empty output: nothing launched
     assert _lib.strerror(_lib.E_ARG).decode().startswith("f16acc")
     a = args
+    assert _lib.gemm_bias(8, 8, None, 8, None, a["M"], a["N"], a["K"], a["sam"], a["sak"], a["sbk"], a["sbn"],
+                          a["scm"], a["scn"], 0, 1, None) == _lib.E_ARG  # bias entry without a bias
     for bad_tile in (-1, len(_lib.TILES), 99):  # forced tile out of range
         assert _lib.gemm_tile(8, 8, 8, None, a["M"], a["N"], a["K"], a["sam"], a["sak"], a["sbk"], a["sbn"],
                               a["scm"], a["scn"], 0, 1, None, bad_tile) == _lib.E_ARG

@@ -249,3 +249,30 @@ def test_overflow_stress_flags_exactly_the_block_intersections():
     mask = flags.bool().repeat_interleave(bm, 0).repeat_interleave(bn, 1)[:1024, :1024]
     assert torch.equal(c[mask], c32[mask])
     assert rel(c.cpu()[~mask.cpu()], ref[~mask.cpu()]) < TOL
+
+
+@pytest.mark.parametrize("shape", [(256, 384, 640), (300, 1000, 77), (1024, 1536, 256), (128, 0, 16)])
+def test_fused_bias_equals_unfused_add_bit_for_bit(shape):
+    """The patched nn.Linear adds its bias in the GEMM's store; the result must
+    equal the reference's unfused y = mm(x2, w.t()); y += b exactly
+    (f16acc/patch.py:28-30), including K = 0 (the zero-width layer)."""
+    from f16acc_amd import patch
+
+    M, K, N = shape
+    x, w, bias = rnd((M, K), 50).cuda(), rnd((N, K), 51, 0.05).cuda(), rnd((N,), 52, 0.5).cuda()
+    unfused = f16acc.mm(x, w.t())
+    unfused += bias
+    with torch.no_grad():
+        fused = patch.linear(x, w, bias)
+    assert torch.equal(fused, unfused)
+
+
+def test_fused_bias_fp32_output_matches_oracle():
+    from f16acc_amd.kernel import mm_bias
+
+    a, w, bias = rnd((300, 520), 53), rnd((200, 520), 54), rnd((200,), 55)
+    c = mm_bias(a.cuda(), w.cuda().t(), bias.cuda(), torch.float32)
+    ref = chunk32.mm(a, w.t(), torch.float32, tile=(128, 128)) + bias.float()
+    assert rel(c.cpu(), ref) < TOL
+    with pytest.raises(ValueError):
+        mm_bias(a.cuda(), w.cuda().t(), bias[:10].cuda())
