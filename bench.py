@@ -131,11 +131,14 @@ def cpu_baseline(a, b, out_dtype, budget_s=20.0):
     return info, ref
 
 
-def sweep_tiles(names):
+def sweep_tiles(names, rounds=5):
     """Time every tile configuration (forced) on the given workloads, chunked,
-    next to the per-shape table's choice and hipBLASLt: the evidence behind
-    the table, as the reference's autotuner times its CONFIGS
-    (f16acc/kernel.py:16-19)."""
+    next to the op as shipped (table choice, packing included) and hipBLASLt:
+    the evidence behind the per-shape table, as the reference's autotuner
+    times its CONFIGS (f16acc/kernel.py:16-19).  The candidates are timed in
+    interleaved rounds (3 warm-up + 5 timed calls each, median over rounds)
+    so the GPU's power-state drift falls on all of them alike."""
+    import f16acc_amd
     from f16acc_amd import _lib
     from f16acc_amd.kernel import mm_tile, tile_config
 
@@ -143,21 +146,33 @@ def sweep_tiles(names):
         M, N, K, layout, out_dtype = WORKLOADS[name]
         _, _, a, b = make_inputs(M, N, K, layout)
         flops = 2.0 * M * N * K
+        ops = {tile: (lambda t=tile: mm_tile(a, b, t, out_dtype)) for tile in _lib.TILES
+               if tile_config(a, b, tile)["tile"] == tile}  # tiles the operands allow
+        ops["mm"] = lambda: f16acc_amd.mm(a, b, out_dtype)
+        ops["hipblaslt"] = lambda: torch.mm(a, b)
+        times = {k: [] for k in ops}
+        for _ in range(rounds):
+            for k, op in ops.items():
+                times[k].append(burst_time(op))
         row = {"workload": name, "M": M, "N": N, "K": K, "b": layout, "table": tile_config(a, b)["tile"]}
-        for tile in _lib.TILES:
-            if tile_config(a, b, tile)["tile"] != tile:
-                continue  # the operands do not allow this tile
-            t = median_event_time(lambda: mm_tile(a, b, tile, out_dtype), iters=20, warmup=5)
-            row[tile] = round(flops / t / 1e12, 1)
-        import f16acc_amd
-
-        t = median_event_time(lambda: f16acc_amd.mm(a, b, out_dtype), iters=20, warmup=5)
-        row["mm"] = round(flops / t / 1e12, 1)  # the op as shipped: table choice, packing included
-        t = median_event_time(lambda: torch.mm(a, b), iters=20, warmup=5)
-        row["hipblaslt"] = round(flops / t / 1e12, 1)
+        row.update({k: round(flops / statistics.median(v) / 1e12, 1) for k, v in times.items()})
         print(json.dumps(row), flush=True)
         del a, b
         torch.cuda.empty_cache()
+
+
+def burst_time(op, warmup=3, calls=5):
+    """Seconds per call over a short back-to-back burst (HIP events)."""
+    for _ in range(warmup):
+        op()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(calls):
+        op()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / 1e3 / calls
 
 
 def overflow_inputs(n=4096, blocks=7, block=128, seed=0):

@@ -608,17 +608,15 @@ inline int fast_layout(int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t s
   return -1;
 }
 
-// Relative throughput of one CU on each fast tile (its chunked MFMA work
-// rate, 128x128 running two workgroups per CU), from tile sweeps on MI355X
-// (4096^3, 8192^3 and the Qwen2.5-1.5B layer shapes), used to compare tile
-// choices for a shape.  Workgroups spread over the CUs, so a CU ends up with
-// ceil(tiles / CUs) tiles:
+// Relative throughput of one CU on each fast tile: its chunked MFMA work rate
+// in steady state (40 ms bursts, after the GPU's power management settles;
+// 128x128 runs two workgroups per CU), measured on MI355X at 4096^3, 8192^3
+// and the Qwen2.5-1.5B layer shapes.  Workgroups spread over the CUs, so a CU
+// ends up with ceil(tiles / CUs) tiles:
 //   estimated time = ceil(tiles / CUs) x tile area / rate.
-// A 256x256 workgroup holds its CU alone, so with fewer than two tiles per
-// CU nothing hides its load latency and barrier waits: its rate drops to
-// ~0.78 of the loaded rate (4096^3: 655 against 856 TFLOPS at 8192^3).
-constexpr double kTileRate[4] = {1.00, 0.90, 0.92, 0.94};
-constexpr double kLoneBigTile = 0.78;
+// 256x256 reads the least LDS per MFMA (64x128 per wave) and wins whenever
+// its tiles fill the machine; smaller tiles win on shapes with few tiles.
+constexpr double kTileRate[4] = {1.00, 0.87, 0.87, 0.89};
 
 // The per-shape table: the fast tile with the smallest estimated time.
 // Ties keep the larger tile.
@@ -628,9 +626,7 @@ inline int choose_tile(int64_t M, int64_t N, int cus) {
   for (int id = 0; id < 4; ++id) {
     const TileInfo& t = kTiles[id];
     const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
-    double rate = kTileRate[id];
-    if (id == 0 && tiles < 2 * (int64_t)cus) rate *= kLoneBigTile;
-    const double est = (double)cdiv(tiles, cus) * t.bm * t.bn / rate;
+    const double est = (double)cdiv(tiles, cus) * t.bm * t.bn / kTileRate[id];
     if (id == 0 || est < best_t * 0.999) {
       best = id;
       best_t = est;

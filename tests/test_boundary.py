@@ -102,9 +102,10 @@ class _Fake:
 
 
 @pytest.mark.parametrize("M,N,K,sa,sb,fam,tile", [
-    (4096, 4096, 4096, (4096, 1), (4096, 1), "fast", "128x128"),   # row-major b (NC loader); one
-    (4096, 4096, 4096, (4096, 1), (1, 4096), "fast", "128x128"),   # 256-tile per CU loses to 128
-    (8192, 8192, 8192, (8192, 1), (8192, 1), "fast", "256x256"),   # four 256-tiles per CU
+    (4096, 4096, 4096, (4096, 1), (4096, 1), "fast", "256x256"),   # row-major b (NC loader)
+    (4096, 4096, 4096, (4096, 1), (1, 4096), "fast", "256x256"),   # w.t() (KC loader)
+    (8192, 8192, 8192, (8192, 1), (8192, 1), "fast", "256x256"),
+    (2048, 151936, 1536, (1536, 1), (1, 1536), "fast", "256x256"),  # lm_head
     (2048, 8960, 1536, (1536, 1), (1, 1536), "fast", "128x128"),   # 280 256-tiles: ragged 2nd wave
     (2048, 1536, 1536, (1536, 1), (1, 1536), "fast", "128x128"),   # too few 256-tiles to fill the CUs
     (2049, 1537, 8961, (8961, 1), (1, 8961), "generic", "generic"),  # rows not 16-byte aligned
