@@ -198,9 +198,10 @@ def overflow_inputs(n=4096, blocks=7, block=128, seed=0):
 def overflow_bench(steps, warmup):
     """Overflow stress workload: chunked time with ~5 % of tiles redone in
     FP32, the same call on the no-overflow data, flagged tiles, and the check
-    that every redone tile equals the FP32-accumulate mode bit for bit."""
+    that every redone tile equals the FP32-accumulate mode (same tile, K not
+    split) bit for bit."""
     import f16acc_amd
-    from f16acc_amd.kernel import mm_flags, tile_config
+    from f16acc_amd.kernel import mm_flags, mm_tile, tile_config
 
     a_cpu, b_cpu, rows, cols = overflow_inputs()
     a, b = a_cpu.cuda(), b_cpu.cuda()
@@ -211,7 +212,7 @@ def overflow_bench(steps, warmup):
     _, ev = time_steps(lambda: f16acc_amd.mm(a, b, torch.float32), steps, warmup)
     t_over = ev / steps
     c, flags = mm_flags(a, b, torch.float32)
-    c32 = f16acc_amd.mm(a, b, torch.float32, chunked=False)
+    c32 = mm_tile(a, b, cfg["tile"], torch.float32, chunked=False)  # unsplit: the redo's summation order
     _, _, ca, cb = make_inputs(M, N, K, "row")
     _, ev = time_steps(lambda: f16acc_amd.mm(ca, cb, torch.float32), steps, warmup)
     t_clean = ev / steps

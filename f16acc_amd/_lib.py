@@ -26,6 +26,14 @@ gemm_bias = _dll.f16acc_gemm_bias
 gemm_bias.argtypes = [_vp, _vp, _vp, _vp, _vp] + [_i64] * 9 + [_int, _int, _vp]
 gemm_bias.restype = _int
 
+gemm_ws = _dll.f16acc_gemm_ws
+gemm_ws.argtypes = [_vp, _vp, _vp, _vp, _vp] + [_i64] * 9 + [_int, _int, _vp, _vp, ctypes.c_size_t]
+gemm_ws.restype = _int
+
+workspace_size = _dll.f16acc_workspace_size
+workspace_size.argtypes = [_i64] * 7 + [_vp, _vp, ctypes.POINTER(ctypes.c_size_t)]
+workspace_size.restype = _int
+
 gemm_tile = _dll.f16acc_gemm_tile
 gemm_tile.argtypes = [_vp, _vp, _vp, _vp] + [_i64] * 9 + [_int, _int, _vp, _int]
 gemm_tile.restype = _int
@@ -51,7 +59,7 @@ abi_version.argtypes = []
 abi_version.restype = _int
 
 # Exported symbol names, as declared in include/f16acc.h.
-EXPORTS = ("f16acc_gemm", "f16acc_gemm_bias", "f16acc_gemm_tile", "f16acc_pack", "f16acc_tile_config", "f16acc_block_tile", "f16acc_strerror",
+EXPORTS = ("f16acc_gemm", "f16acc_gemm_bias", "f16acc_gemm_ws", "f16acc_workspace_size", "f16acc_gemm_tile", "f16acc_pack", "f16acc_tile_config", "f16acc_block_tile", "f16acc_strerror",
            "f16acc_abi_version")
 ABI_VERSION = 2
 

@@ -72,7 +72,21 @@ struct Params {
   int64_t sam, sak, sbk, sbn, scm, scn;
   int64_t tiles_m, tiles_n;
   int vec_store;  // c rows are contiguous and 16-byte aligned in 4-element groups
+  // Split-K runs two launches.  kPartial: workgroup (tile, s) sums the K
+  // range [s * kps, (s + 1) * kps) (kps a whole number of stages, so chunks
+  // stay whole) and writes its FP32 partial to ws.  kFinish (the next launch,
+  // so the partials are visible without any fence): one workgroup per tile
+  // adds them in split order and flags, redoes and stores the tile.
+  int mode;
+  int splits;
+  int64_t kps;
+  float* ws;  // tiles * splits * BM * BN floats
 };
+
+enum Mode { kWhole = 0, kPartial = 1, kFinish = 2 };
+template <class C, bool CHUNKED>
+__device__ __forceinline__ void k_loop_generic(const Params& p, int64_t m0, int64_t n0, char LDS_AS* smem,
+                                               int tid, int wm, int wn, int lane, f32x4 (&acc)[C::FM][C::FN]);
 
 // ---------------------------------------------------------------------------
 // Workgroup -> output tile.  Workgroups are dispatched round-robin over the
@@ -82,17 +96,23 @@ struct Params {
 // column-major inside a group, as the reference's _tile does,
 // kernel.py:26-29) so one XCD's tiles share A rows and B columns.
 // ---------------------------------------------------------------------------
-__host__ __device__ inline void block_tile(int64_t block, int64_t tiles_m, int64_t tiles_n,
-                                           int64_t* tm, int64_t* tn) {
-  const int64_t total = tiles_m * tiles_n;
+__host__ __device__ inline int64_t xcd_order(int64_t block, int64_t total) {
   const int64_t x = block % kNumXcd, l = block / kNumXcd;
   const int64_t q = total / kNumXcd, r = total % kNumXcd;
-  const int64_t id = x < r ? x * (q + 1) + l : r * (q + 1) + (x - r) * q + l;
+  return x < r ? x * (q + 1) + l : r * (q + 1) + (x - r) * q + l;
+}
+
+__host__ __device__ inline void group_m(int64_t id, int64_t tiles_m, int64_t tiles_n, int64_t* tm, int64_t* tn) {
   const int64_t width = kGroupM * tiles_n;
   const int64_t first = (id / width) * kGroupM;
   const int64_t gsz = tiles_m - first < kGroupM ? tiles_m - first : kGroupM;
   *tm = first + (id % width) % gsz;
   *tn = (id % width) / gsz;
+}
+
+__host__ __device__ inline void block_tile(int64_t block, int64_t tiles_m, int64_t tiles_n, int64_t* tm,
+                                           int64_t* tn) {
+  group_m(xcd_order(block, tiles_m * tiles_n), tiles_m, tiles_n, tm, tn);
 }
 
 // LDS swizzles (see the header comment).  kc_swz spreads the 16 rows one
@@ -121,6 +141,10 @@ struct Cfg {
   static_assert(BM * 8 % T == 0 && BN * 8 % T == 0, "stage must split evenly over threads");
   static_assert(BL == kKC || BN >= 128, "NC swizzle needs at least 16 units per k-row");
   static_assert(NS >= 2 && NS * STAGE <= 160 * 1024, "LDS ring must fit the 160 KiB of a CU");
+  // Split-K partial stores are compiled only into tiles of 64x64 per wave:
+  // at 64x128 per wave the chunked kernel already uses ~240 of its 256
+  // registers, and the extra path would make it spill.
+  static constexpr bool SPLITTABLE = FM * FN <= 16;
   static_assert((NS - 2) * (LA + LB) <= 63, "outstanding loads must fit vmcnt");
 };
 
@@ -199,9 +223,9 @@ struct FastLoader {
   }
 
   // Issue the global -> LDS copies of the stage starting at k = kbase.
-  __device__ void issue(const Params& p, int64_t m0, int64_t n0, int64_t kbase, char LDS_AS* stage,
+  __device__ void issue(const Params& p, int64_t m0, int64_t n0, int64_t kbase, int64_t kend, char LDS_AS* stage,
                         int wave) {
-    const int64_t krem = p.K - kbase;  // k < krem is inside the matrix
+    const int64_t krem = kend - kbase;  // k < krem is inside this workgroup's K range
     const i32x4 ra = make_srd(p.a + (m0 * p.sam + kbase));
     const i32x4 rb = C::BL == kKC ? make_srd(p.b + (n0 * p.sbn + kbase)) : make_srd(p.b + (kbase * p.sbk + n0));
     const int lds = __builtin_amdgcn_readfirstlane((int)(uint32_t)(size_t)stage + wave * 64 * 16);
@@ -347,14 +371,14 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
 // wave's copies visible and retires all reads of the slot stage s+NS-1 will
 // overwrite, then that copy is issued and stage s is multiplied.
 template <class C, bool CHUNKED>
-__device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t n0, char LDS_AS* smem,
-                                            FastLoader<C>& ld, int tid, int wave, int wm, int wn, int lane,
-                                            f32x4 (&acc)[C::FM][C::FN]) {
-  const int64_t nsteps = (p.K + kStageK - 1) / kStageK;
-  if (nsteps == 0) return;
+__device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t n0, int64_t kbeg, int64_t kend,
+                                            char LDS_AS* smem, FastLoader<C>& ld, int tid, int wave, int wm, int wn,
+                                            int lane, f32x4 (&acc)[C::FM][C::FN]) {
+  const int64_t nsteps = (kend - kbeg + kStageK - 1) / kStageK;
+  if (nsteps <= 0) return;
 #pragma unroll
   for (int s0 = 0; s0 < C::NS - 1; ++s0)
-    if (s0 < nsteps) ld.issue(p, m0, n0, (int64_t)s0 * kStageK, smem + s0 * C::STAGE, wave);
+    if (s0 < nsteps) ld.issue(p, m0, n0, kbeg + (int64_t)s0 * kStageK, kend, smem + s0 * C::STAGE, wave);
   int slot = 0;
   for (int64_t s = 0; s < nsteps; ++s) {
     if (s + C::NS - 2 < nsteps)
@@ -365,7 +389,7 @@ __device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t
     const int64_t nxt = s + C::NS - 1;
     if (nxt < nsteps) {
       const int nslot = slot == 0 ? C::NS - 1 : slot - 1;  // (s + NS - 1) % NS
-      ld.issue(p, m0, n0, nxt * kStageK, smem + nslot * C::STAGE, wave);
+      ld.issue(p, m0, n0, kbeg + nxt * kStageK, kend, smem + nslot * C::STAGE, wave);
     }
     compute_stage<C, CHUNKED>(smem + slot * C::STAGE, wm, wn, lane, acc);
     slot = slot + 1 == C::NS ? 0 : slot + 1;
@@ -470,10 +494,56 @@ __device__ __forceinline__ void store_tile(const Params& p, int64_t m0, int64_t 
   }
 }
 
-// One kernel body for both families: FAST selects the direct-to-LDS loader.
-// amdgpu_waves_per_eu(2) caps a wave at 256 registers, which keeps every MFMA
-// in its VGPR form: the chunk partials are read by VALU conversions, and an
-// AGPR destination would cost a v_accvgpr_read per register.
+// Flag, redo and store of a finished FP32 tile sum (shared by the whole-K
+// kernel and the split-K finishing kernel).
+template <class C, bool FAST, bool CHUNKED, bool OUT32>
+__device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, FastLoader<C>& ld, int* tile_bad,
+                                            int64_t tm, int64_t tn, int tid, int wave, int wm, int wn, int lane,
+                                            f32x4 (&acc)[C::FM][C::FN]) {
+  const int64_t m0 = tm * C::BM, n0 = tn * C::BN;
+  if (CHUNKED) {
+    // tile flag: any element of the FP32 sum inf or NaN (kernel.py:70-71)
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bad |= !(__builtin_fabsf(acc[i][j][r]) < __builtin_inff());
+    if (bad) *tile_bad = 1;
+    __syncthreads();
+    const int flag = *tile_bad;
+    if (p.flags && tid == 0) p.flags[tm * p.tiles_n + tn] = (uint8_t)flag;
+    if (flag) {
+      // redo the whole tile, all of K, with FP32 accumulation (kernel.py:75-81)
+#pragma unroll
+      for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (FAST)
+        k_loop_fast<C, false>(p, m0, n0, 0, p.K, smem, ld, tid, wave, wm, wn, lane, acc);
+      else
+        k_loop_generic<C, false>(p, m0, n0, smem, tid, wm, wn, lane, acc);
+    }
+  }
+  store_tile<C, OUT32>(p, m0, n0, wm, wn, lane, acc);
+}
+
+// FP32 partials of a split tile, thread-private order: split s, block
+// (i, j) of thread tid is the 16-byte unit at float offset
+// s * BM * BN + ((i * FN + j) * T + tid) * 4 (consecutive threads write and
+// read consecutive units).  Whole f32x4 vectors are stored and loaded: this
+// hipcc miscompiles one-by-one element extraction feeding a buffer store.
+template <class C>
+__device__ __forceinline__ int part_offset(int i, int j, int tid) {
+  return ((i * C::FN + j) * C::T + tid) * 4;
+}
+
+// Whole-K (kWhole) and split-K partial (kPartial) kernel; FAST selects the
+// direct-to-LDS loader.  amdgpu_waves_per_eu(2) caps a wave at 256
+// registers, which keeps every MFMA in its VGPR form: the chunk partials are
+// read by VALU conversions, and an AGPR destination would cost a
+// v_accvgpr_read per register.
 template <class C, bool FAST, bool CHUNKED, bool OUT32>
 __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(Params p) {
   __shared__ __attribute__((aligned(1024))) char smem_raw[FAST ? C::NS * C::STAGE : C::STAGE];
@@ -483,9 +553,17 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+  // block -> (tile, K split): the XCD renumbering keeps a tile's splits together
+  const int64_t tiles = p.tiles_m * p.tiles_n;
+  const int nsplit = C::SPLITTABLE && p.mode == kPartial ? p.splits : 1;
+  const int64_t id = xcd_order(blockIdx.x, tiles * nsplit);
+  const int64_t tile = id / nsplit;
+  const int split = (int)(id % nsplit);
   int64_t tm, tn;
-  block_tile(blockIdx.x, p.tiles_m, p.tiles_n, &tm, &tn);
+  group_m(tile, p.tiles_m, p.tiles_n, &tm, &tn);
   const int64_t m0 = tm * C::BM, n0 = tn * C::BN;
+  const int64_t kbeg = nsplit > 1 ? split * p.kps : 0;
+  const int64_t kend = nsplit > 1 && kbeg + p.kps < p.K ? kbeg + p.kps : p.K;
 
   if (CHUNKED && tid == 0) tile_bad = 0;
 
@@ -498,37 +576,60 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void 
   FastLoader<C> ld;
   if (FAST) {
     ld.init(p, m0, n0, tid);
-    k_loop_fast<C, CHUNKED>(p, m0, n0, smem, ld, tid, wave, wm, wn, lane, acc);
+    k_loop_fast<C, CHUNKED>(p, m0, n0, kbeg, kend, smem, ld, tid, wave, wm, wn, lane, acc);
   } else {
     k_loop_generic<C, CHUNKED>(p, m0, n0, smem, tid, wm, wn, lane, acc);
   }
 
-  if (CHUNKED) {
-    // tile flag: any element of the FP32 sum inf or NaN (kernel.py:70-71)
-    bool bad = false;
+  if (C::SPLITTABLE && p.mode == kPartial) {
+    // buffer stores: one lane offset register and a scalar offset per
+    // element, instead of a 64-bit address per store
+    float* mine = p.ws + (tile * p.splits + split) * (int64_t)(C::BM * C::BN);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(mine, (short)0, C::BM * C::BN * (int)sizeof(float), 0x00020000);
 #pragma unroll
     for (int i = 0; i < C::FM; ++i)
 #pragma unroll
       for (int j = 0; j < C::FN; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) bad |= !(__builtin_fabsf(acc[i][j][r]) < __builtin_inff());
-    if (bad) tile_bad = 1;
-    __syncthreads();
-    const int flag = tile_bad;
-    if (p.flags && tid == 0) p.flags[tm * p.tiles_n + tn] = (uint8_t)flag;
-    if (flag) {
-      // redo the whole tile with FP32 accumulation (kernel.py:75-81)
-#pragma unroll
-      for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (FAST)
-        k_loop_fast<C, false>(p, m0, n0, smem, ld, tid, wave, wm, wn, lane, acc);
-      else
-        k_loop_generic<C, false>(p, m0, n0, smem, tid, wm, wn, lane, acc);
-    }
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, acc[i][j]), rs, tid * 16,
+                                               part_offset<C>(i, j, 0) * 4, 0);
+    return;
   }
-  store_tile<C, OUT32>(p, m0, n0, wm, wn, lane, acc);
+  finish_tile<C, FAST, CHUNKED, OUT32>(p, smem, ld, &tile_bad, tm, tn, tid, wave, wm, wn, lane, acc);
+}
+
+// Split-K finishing kernel (kFinish): one workgroup per tile adds the FP32
+// partials in split order, ((p_0 + p_1) + p_2) + ..., deterministic whatever
+// order the partial launch ran in, then flags / redoes / stores the tile.
+// Its redo (rare: only an overflowing tile) gathers the operands through the
+// generic strided path, so C is the K-contiguous variant of the tile shape.
+template <class C, bool CHUNKED, bool OUT32>
+__global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void finish_kernel(Params p) {
+  __shared__ __attribute__((aligned(1024))) char smem_raw[C::STAGE];
+  __shared__ int tile_bad;
+  char LDS_AS* smem = (char LDS_AS*)smem_raw;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+  const int64_t tile = xcd_order(blockIdx.x, p.tiles_m * p.tiles_n);
+  int64_t tm, tn;
+  group_m(tile, p.tiles_m, p.tiles_n, &tm, &tn);
+  if (CHUNKED && tid == 0) tile_bad = 0;
+  const float* part = p.ws + tile * p.splits * (int64_t)(C::BM * C::BN);
+  f32x4 acc[C::FM][C::FN];
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) acc[i][j] = *(const f32x4*)(part + part_offset<C>(i, j, tid));
+  for (int s = 1; s < p.splits; ++s) {
+    const float* ps = part + (int64_t)s * C::BM * C::BN;
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j) acc[i][j] += *(const f32x4*)(ps + part_offset<C>(i, j, tid));
+  }
+  FastLoader<C> unused;
+  finish_tile<C, false, CHUNKED, OUT32>(p, smem, unused, &tile_bad, tm, tn, tid, wave, wm, wn, lane, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -650,7 +751,7 @@ inline Choice choose(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, 
 
 template <class C, bool FAST>
 hipError_t launch_cfg(const Params& p, int out32, int chunked, hipStream_t st) {
-  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(C::T);
+  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * (p.mode == kPartial ? p.splits : 1))), block(C::T);
   if (chunked) {
     if (out32)
       hipLaunchKernelGGL((gemm_kernel<C, FAST, true, true>), grid, block, 0, st, p);
@@ -671,9 +772,61 @@ hipError_t launch_fast(const Params& p, int blayout, int out32, int chunked, hip
                         : launch_cfg<CF<kNC>, true>(p, out32, chunked, st);
 }
 
+template <template <int> class CF>
+hipError_t launch_finish(const Params& p, int out32, int chunked, hipStream_t st) {
+  using C = CF<kKC>;
+  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(C::T);
+  if (chunked) {
+    if (out32)
+      hipLaunchKernelGGL((finish_kernel<C, true, true>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((finish_kernel<C, true, false>), grid, block, 0, st, p);
+  } else {
+    if (out32)
+      hipLaunchKernelGGL((finish_kernel<C, false, true>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((finish_kernel<C, false, false>), grid, block, 0, st, p);
+  }
+  return hipGetLastError();
+}
+
+// Split-K plan: when a shape has fewer tiles than the CUs can hold, split K
+// into chunk-aligned ranges so the workgroups fill the machine.  The second
+// launch and the partials' traffic only pay off on long K (measured: the
+// Qwen2.5 down projection, K = 8960, gains; K = 1536 loses), so each split
+// keeps at least kMinSplitStages LDS stages; at most kMaxSplits.
+constexpr int kMaxSplits = 16;
+constexpr int kMinSplitStages = 16;
+
+struct SplitPlan {
+  int splits;
+  int64_t kps;   // K per split, a multiple of kStageK
+  size_t bytes;  // workspace for the FP32 partials (0: no split)
+};
+
+inline SplitPlan plan_split(const Choice& ch, int64_t M, int64_t N, int64_t K, int cus) {
+  SplitPlan sp{1, K, 0};
+  if (ch.family != F16ACC_FAMILY_FAST || ch.tile == F16ACC_TILE_256x256) return sp;  // not SPLITTABLE
+  const TileInfo& t = kTiles[ch.tile];
+  const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
+  const int64_t slots = (int64_t)cus * t.per_cu;
+  const int64_t nsteps = cdiv(K, kStageK);
+  int64_t want = slots / tiles;
+  if (want > kMaxSplits) want = kMaxSplits;
+  if (want > nsteps / kMinSplitStages) want = nsteps / kMinSplitStages;
+  if (want < 2) return sp;
+  const int64_t steps_per = cdiv(nsteps, want);
+  const int64_t splits = cdiv(nsteps, steps_per);
+  if (splits < 2) return sp;
+  sp.splits = (int)splits;
+  sp.kps = steps_per * kStageK;
+  sp.bytes = (size_t)tiles * splits * t.bm * t.bn * sizeof(float);
+  return sp;
+}
+
 int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* tile_flags, int64_t M, int64_t N,
               int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int out_dtype,
-              int chunked, void* stream, int forced_tile) {
+              int chunked, void* stream, int forced_tile, void* workspace = nullptr, size_t ws_bytes = 0) {
   if (M < 0 || N < 0 || K < 0) return F16ACC_E_ARG;
   if (out_dtype != F16ACC_OUT_F16 && out_dtype != F16ACC_OUT_F32) return F16ACC_E_ARG;
   if (chunked != 0 && chunked != 1) return F16ACC_E_ARG;
@@ -693,15 +846,38 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
   p.tiles_n = cdiv(N, kTiles[ch.tile].bn);
   const int esize = out_dtype == F16ACC_OUT_F32 ? 4 : 2;
   p.vec_store = scn == 1 && (scm * esize) % 16 == 0 && ((uintptr_t)c % 16) == 0;
-  if (p.tiles_m * p.tiles_n > 0x7fffffff) return F16ACC_E_UNSUPPORTED;
+  p.mode = kWhole;
+  p.splits = 1;
+  p.kps = K;
+  p.ws = nullptr;
+  if (workspace) {
+    const SplitPlan sp = plan_split(ch, M, N, K, cu_count());
+    if (sp.splits > 1 && ws_bytes >= sp.bytes) {
+      p.mode = kPartial;
+      p.splits = sp.splits;
+      p.kps = sp.kps;
+      p.ws = (float*)workspace;
+    }
+  }
+  if (p.tiles_m * p.tiles_n * p.splits > 0x7fffffff) return F16ACC_E_UNSUPPORTED;
   const int out32 = out_dtype == F16ACC_OUT_F32;
   hipStream_t st = (hipStream_t)stream;
-  switch (ch.tile) {
-    case 0: return (int)launch_fast<Cfg0>(p, ch.blayout, out32, chunked, st);
-    case 1: return (int)launch_fast<Cfg1>(p, ch.blayout, out32, chunked, st);
-    case 2: return (int)launch_fast<Cfg2>(p, ch.blayout, out32, chunked, st);
-    case 3: return (int)launch_fast<Cfg3>(p, ch.blayout, out32, chunked, st);
-    default: return (int)launch_cfg<CfgG, false>(p, out32, chunked, st);
+  auto launch = [&](const Params& q) -> int {
+    switch (ch.tile) {
+      case 0: return (int)launch_fast<Cfg0>(q, ch.blayout, out32, chunked, st);
+      case 1: return (int)launch_fast<Cfg1>(q, ch.blayout, out32, chunked, st);
+      case 2: return (int)launch_fast<Cfg2>(q, ch.blayout, out32, chunked, st);
+      case 3: return (int)launch_fast<Cfg3>(q, ch.blayout, out32, chunked, st);
+      default: return (int)launch_cfg<CfgG, false>(q, out32, chunked, st);
+    }
+  };
+  int rc = launch(p);
+  if (rc != 0 || p.mode != kPartial) return rc;
+  p.mode = kFinish;
+  switch (ch.tile) {  // 256x256 never splits (plan_split)
+    case 1: return (int)launch_finish<Cfg1>(p, out32, chunked, st);
+    case 2: return (int)launch_finish<Cfg2>(p, out32, chunked, st);
+    default: return (int)launch_finish<Cfg3>(p, out32, chunked, st);
   }
 }
 
@@ -773,6 +949,24 @@ int f16acc_pack(const void* src, void* dst, int64_t rows, int64_t cols, int64_t 
     hipLaunchKernelGGL(pack_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
                        (const f16*)src, (f16*)dst, rows, cols, s_r, s_c, rows_pad, ld);
   return (int)hipGetLastError();
+}
+
+int f16acc_workspace_size(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                          const void* a, const void* b, size_t* bytes) {
+  if (M < 0 || N < 0 || K < 0 || !bytes) return F16ACC_E_ARG;
+  *bytes = 0;
+  if (M == 0 || N == 0) return 0;
+  const Choice ch = choose(M, N, K, sam, sak, sbk, sbn, a, b, -1);
+  *bytes = plan_split(ch, M, N, K, cu_count()).bytes;
+  return 0;
+}
+
+int f16acc_gemm_ws(const void* a, const void* b, const void* bias, void* c, uint8_t* tile_flags, int64_t M,
+                   int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn,
+                   int out_dtype, int chunked, void* stream, void* workspace, size_t ws_bytes) {
+  if (workspace && ((uintptr_t)workspace % 256) != 0) return F16ACC_E_ARG;
+  return gemm_impl(a, b, bias, c, tile_flags, M, N, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked, stream, -1,
+                   workspace, ws_bytes);
 }
 
 int f16acc_gemm_tile(const void* a, const void* b, void* c, uint8_t* tile_flags, int64_t M, int64_t N, int64_t K,

@@ -22,6 +22,13 @@ _OUT = {torch.float16: _lib.OUT_F16, torch.float32: _lib.OUT_F32}
 # kernel (the copy's launch and traffic are not repaid).
 PACK_MIN_MACS = 1 << 24
 
+# Split-K workspace for the FP32 partials, one per (device, stream): kernels
+# on one stream run one after another, so consecutive calls on a stream can
+# share it.
+_workspaces = {}
+_ws_sizes = {}  # problem key -> f16acc_workspace_size result
+_WS_MEMO_MAX = 4096
+
 
 def _validate(a, b, out_dtype):
     """Real checks, not asserts (python -O keeps them): a wrong shape or dtype
@@ -50,8 +57,31 @@ def mm(a, b, out_dtype=torch.float16, chunked=True):
     if M == 0 or N == 0:
         return c
     a, b, K = _operands(a, b, M, N, K)
-    _launch(a, b, c, None, M, N, K, chunked)
+    _launch(a, b, c, None, M, N, K, chunked, ws=_workspace(a, b, M, N, K))
     return c
+
+
+def _workspace(a, b, M, N, K):
+    """The split-K workspace for this problem on the current stream, or None
+    when the library would not split it (its tiles already fill the GPU)."""
+    key = (a.device.index, M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1), a.data_ptr() % 16,
+           b.data_ptr() % 16)
+    nbytes = _ws_sizes.get(key)
+    if nbytes is None:
+        n = ctypes.c_size_t()
+        _lib.check(_lib.workspace_size(M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1), a.data_ptr(),
+                                       b.data_ptr(), ctypes.byref(n)))
+        if len(_ws_sizes) >= _WS_MEMO_MAX:
+            _ws_sizes.clear()
+        nbytes = _ws_sizes[key] = n.value
+    if nbytes == 0:
+        return None
+    skey = (a.device.index, torch.cuda.current_stream(a.device).cuda_stream)
+    ws = _workspaces.get(skey)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=a.device)
+        _workspaces[skey] = ws
+    return ws
 
 
 def mm_bias(a, b, bias, out_dtype=torch.float16, chunked=True):
@@ -71,7 +101,7 @@ def mm_bias(a, b, bias, out_dtype=torch.float16, chunked=True):
     if M == 0 or N == 0:
         return c
     a, b, K = _operands(a, b, M, N, K)
-    _launch(a, b, c, None, M, N, K, chunked, bias=bias.contiguous())
+    _launch(a, b, c, None, M, N, K, chunked, bias=bias.contiguous(), ws=_workspace(a, b, M, N, K))
     return c
 
 
@@ -133,7 +163,8 @@ def mm_flags(a, b, out_dtype=torch.float16, chunked=True, tile=None):
     cfg = tile_config(a, b, tile)
     flags = torch.zeros(cfg["tiles_m"], cfg["tiles_n"], device=a.device, dtype=torch.uint8)
     if M and N:
-        _launch(a, b, c, flags, M, N, K, chunked, _tile_id(tile))
+        ws = _workspace(a, b, M, N, K) if tile is None else None
+        _launch(a, b, c, flags, M, N, K, chunked, _tile_id(tile), ws=ws)
     return c, flags
 
 
@@ -173,16 +204,19 @@ def tile_config(a, b, tile=None):
             "tiles_n": tn.value, "family": ("fast", "generic")[fam.value], "threads": thr.value}
 
 
-def _launch(a, b, c, flags, M, N, K, chunked, tile=-1, bias=None):
+def _launch(a, b, c, flags, M, N, K, chunked, tile=-1, bias=None, ws=None):
     dev = a.device
     if torch.cuda.current_device() != dev.index:
         with torch.cuda.device(dev):
-            return _launch(a, b, c, flags, M, N, K, chunked, tile, bias)
+            return _launch(a, b, c, flags, M, N, K, chunked, tile, bias, ws)
     stream = torch.cuda.current_stream(dev).cuda_stream
     ptrs = (a.data_ptr(), b.data_ptr(), c.data_ptr(), flags.data_ptr() if flags is not None else None)
     args = (M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1),
             _OUT[c.dtype], int(bool(chunked)), stream)
-    if bias is not None:
+    if ws is not None:
+        rc = _lib.gemm_ws(ptrs[0], ptrs[1], bias.data_ptr() if bias is not None else None, ptrs[2], ptrs[3], *args,
+                          ws.data_ptr(), ws.numel())
+    elif bias is not None:
         rc = _lib.gemm_bias(ptrs[0], ptrs[1], bias.data_ptr(), ptrs[2], ptrs[3], *args)
     elif tile < 0:
         rc = _lib.gemm(*ptrs, *args)

@@ -89,6 +89,34 @@ int f16acc_gemm_bias(const void* a, const void* b, const void* bias, void* c, ui
                      int out_dtype, int chunked, void* stream);
 
 /*
+ * Workspace that lets f16acc_gemm_ws split K for this problem (0 when the
+ * problem's tiles already fill the GPU, or its operands take the generic
+ * path).  Shapes with few output tiles (k/v projections, 2048 x 256) leave
+ * most CUs idle; splitting K into chunk-aligned ranges fills them.
+ */
+int f16acc_workspace_size(int64_t M, int64_t N, int64_t K,
+                          int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                          const void* a, const void* b, size_t* bytes);
+
+/*
+ * f16acc_gemm (bias NULL) or f16acc_gemm_bias (bias non-NULL), splitting K
+ * when `workspace` (256-byte aligned, ws_bytes >= f16acc_workspace_size)
+ * allows it; with a NULL or smaller workspace it does exactly what they do.
+ * A split problem runs two launches on `stream`: workgroups sum K ranges of
+ * whole chunk pairs (so the chunks are the reference's, f16acc/kernel.py:
+ * 44-49) into FP32 partials in the workspace; then one workgroup per tile
+ * adds them in split order, flags the tile when the total is not finite and
+ * recomputes it over all of K with FP32 accumulation (kernel.py:70-81), and
+ * stores it.  The workspace needs no initialisation; calls that overlap in
+ * time need separate workspaces.
+ */
+int f16acc_gemm_ws(const void* a, const void* b, const void* bias, void* c, uint8_t* tile_flags,
+                   int64_t M, int64_t N, int64_t K,
+                   int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                   int64_t scm, int64_t scn,
+                   int out_dtype, int chunked, void* stream, void* workspace, size_t ws_bytes);
+
+/*
  * The tile configuration f16acc_gemm picks for a problem: replaces the
  * reference's autotuned CONFIGS table and best_config handoff
  * (f16acc/kernel.py:16-19, 63, 101-102) with a fixed per-shape table.

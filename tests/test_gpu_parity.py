@@ -231,16 +231,18 @@ def test_odd_config_2049_1537_8961():
 def test_overflow_stress_flags_exactly_the_block_intersections():
     """The overflow stress workload at 1024^2 x 1024 with 2 of 8 row-blocks of
     a and column-blocks of b set to U(200, 255): only the 4 intersection tiles
-    overflow; they are flagged like the oracle's, equal the FP32-accumulate
-    mode bit for bit (same tile, same summation order), and every other tile
-    matches the oracle."""
+    overflow; they are flagged like the oracle's, equal the unsplit
+    FP32-accumulate mode bit for bit (the redo runs all of K in one workgroup:
+    same tile, same summation order), and every other tile matches the
+    oracle."""
     import bench
+    from f16acc_amd.kernel import mm_tile
 
     a, b, rows, cols = bench.overflow_inputs(n=1024, blocks=2)
     ga, gb = a.cuda(), b.cuda()
     cfg = tile_config(ga, gb)
     c, flags = mm_flags(ga, gb, torch.float32)
-    c32 = f16acc.mm(ga, gb, torch.float32, chunked=False)
+    c32 = mm_tile(ga, gb, cfg["tile"], torch.float32, chunked=False)
     ref, rflags = oracle(a, b, torch.float32, cfg)
     assert torch.equal(flags.cpu(), rflags)
     bm, bn = cfg["bm"], cfg["bn"]
@@ -276,3 +278,86 @@ def test_fused_bias_fp32_output_matches_oracle():
     assert rel(c.cpu(), ref) < TOL
     with pytest.raises(ValueError):
         mm_bias(a.cuda(), w.cuda().t(), bias[:10].cuda())
+
+
+def _split_plan(ga, gb):
+    import ctypes
+
+    from f16acc_amd import _lib
+
+    M, K = ga.shape
+    N = gb.shape[1]
+    n = ctypes.c_size_t()
+    _lib.check(_lib.workspace_size(M, N, K, ga.stride(0), ga.stride(1), gb.stride(0), gb.stride(1), ga.data_ptr(),
+                                   gb.data_ptr(), ctypes.byref(n)))
+    return n.value
+
+
+@pytest.mark.parametrize("shape", [(256, 256, 4096), (2048, 256, 4096), (300, 200, 2100), (512, 384, 8960)])
+def test_split_k_matches_oracle(shape):
+    """Shapes with few output tiles are split along K into chunk-aligned
+    ranges; a second launch adds the FP32 partials per tile.  Results and
+    flags match the oracle; repeated calls (sharing the stream's workspace)
+    give identical bits."""
+    M, N, K = shape
+    a, w = rnd((M, K), 60 + K), rnd((N, K), 61 + K)
+    ga, gb = a.cuda(), w.cuda().t()
+    a2, b2, K2, _ = _packed_case(ga, gb)
+    assert _split_plan(a2, b2) > 0, "shape expected to be split"
+    cfg = tile_config(a2, b2)
+    for out_dtype in (torch.float32, torch.float16):
+        c, flags = mm_flags(ga, gb, out_dtype)
+        ref, rflags = oracle(a, w.t(), out_dtype, cfg)
+        assert torch.equal(flags.cpu(), rflags)
+        assert rel(c.cpu(), ref) < TOL, (shape, out_dtype)
+        # the workspace is reused across calls: another split problem in between
+        f16acc.mm(rnd((64, 512), 1).cuda(), rnd((512, 64), 2).cuda())
+        again = f16acc.mm(ga, gb, out_dtype)
+        assert torch.equal(again, c)
+
+
+def test_split_k_overflow_in_one_split_redoes_the_whole_tile():
+    """A chunk overflow inside one K range of a split tile: the summed tile is
+    not finite, so the finishing launch flags it and recomputes it over all of
+    K in FP32, exactly (the reference's closed form, tests/test_f16acc.py:
+    91-101, widened)."""
+    M, N, K = 256, 256, 4096
+    a = rnd((M, K), 70, 0.1)
+    b = rnd((K, N), 71, 0.1)
+    a[10:20, :] = 100.0
+    b[:, 30:40] = 0.0
+    b[2048:2080, 30:40], b[2080:2112, 30:40] = 30.0, -30.0  # chunk sums of +-96000 in one split
+    b[2111, 30:40] = -29.0
+    ga, gb = a.cuda(), b.cuda()
+    assert _split_plan(ga, gb) > 0
+    cfg = tile_config(ga, gb)
+    c, flags = mm_flags(ga, gb, torch.float32)
+    ref, rflags = oracle(a, b, torch.float32, cfg)
+    assert torch.equal(flags.cpu(), rflags) and int(flags.sum()) == 1
+    assert torch.all(c[10:20, 30:40].cpu() == 100.0)
+    assert rel(c.cpu(), ref) < TOL
+
+
+def test_split_k_bias_and_ws_entry_without_workspace():
+    """A biased projection with few output tiles and long K (2048 x 256 x
+    4096) takes the split path through patch.linear and still equals the
+    unfused y = mm(x2, w.t()); y += b bit for bit; f16acc_gemm_ws with no
+    workspace is f16acc_gemm."""
+    from f16acc_amd import _lib, patch
+
+    x, w, bias = rnd((2048, 4096), 72).cuda(), rnd((256, 4096), 73, 0.02).cuda(), rnd((256,), 74, 0.02).cuda()
+    assert _split_plan(x, w.t()) > 0
+    unfused = f16acc.mm(x, w.t())
+    unfused += bias
+    with torch.no_grad():
+        assert torch.equal(patch.linear(x, w, bias), unfused)
+    c = torch.empty(2048, 256, device="cuda", dtype=torch.float16)
+    st = torch.cuda.current_stream().cuda_stream
+    rc = _lib.gemm_ws(x.data_ptr(), w.data_ptr(), None, c.data_ptr(), None, 2048, 256, 4096, x.stride(0), 1,
+                      1, 4096, 256, 1, 0, 1, st, None, 0)
+    assert rc == 0
+    plain = torch.empty_like(c)
+    assert _lib.gemm(x.data_ptr(), w.data_ptr(), plain.data_ptr(), None, 2048, 256, 4096, x.stride(0), 1, 1, 4096,
+                     256, 1, 0, 1, st) == 0
+    assert torch.equal(c, plain)
+    assert rel(c.cpu(), chunk32.mm(x.cpu(), w.cpu().t(), torch.float16, tile=(128, 128))) < TOL
