@@ -294,6 +294,17 @@ __device__ __forceinline__ f16x8 chunk_pair_selector(int lane) {
   return s;
 }
 
+// Half h of round_pair: elements 4h .. 4h+3 of x from lanes r = 2h, 2h+1.
+__device__ __forceinline__ void round_half(const f32x4& p0, const f32x4& p1, f16x8& x, int h) {
+#pragma unroll
+  for (int r = 2 * h; r < 2 * h + 2; ++r) {
+    const f32x2 pr = {p0[r], p1[r]};
+    const f16x2 v = __builtin_convertvector(pr, f16x2);  // v_cvt_pk_f16_f32: RNE, inf past 65504
+    x[2 * r] = v[0];
+    x[2 * r + 1] = v[1];
+  }
+}
+
 __device__ __forceinline__ f16x8 round_pair(const f32x4& p0, const f32x4& p1) {
   f16x8 x;
 #pragma unroll
@@ -313,11 +324,11 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
   const char LDS_AS* bs = stage + C::A_STAGE;
   const int r16 = lane & 15, g = lane >> 4;
   f16x8 af[C::FM][2];
-#pragma unroll
-  for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-    for (int c = 0; c < 2; ++c) af[i][c] = read_kc<C>(as, wm * C::WTM + 16 * i + r16, 4 * c + g);
   if (!CHUNKED) {
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) af[i][c] = read_kc<C>(as, wm * C::WTM + 16 * i + r16, 4 * c + g);
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) {
       const f16x8 b0 = read_b<C>(bs, wn, j, 0, lane), b1 = read_b<C>(bs, wn, j, 1, lane);
@@ -331,32 +342,53 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
     return;
   }
   // Chunked: blocks t = 0 .. FM*FN-1 (i = t % FM fastest), software
-  // pipelined three deep: step t issues the two chunk MFMAs of block t, rounds
-  // the partials of block t-1 and sums block t-2 with the selector MFMA, so
-  // no instruction waits on the MFMA that produced its operand.
+  // pipelined four deep.  Step t issues block t's two chunk MFMAs with the
+  // rounding of block t-2 between them (half after each), then the selector
+  // MFMA of block t-3: every instruction reads an MFMA result at least three
+  // MFMAs old, so nothing waits on the matrix pipe.  sched_barrier fences keep
+  // that order (left to itself the scheduler puts each conversion right
+  // behind the MFMA that produces its input and pads with s_nop).
   constexpr int T = C::FM * C::FN;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   const f16x8 sel = chunk_pair_selector(lane);  // loop invariant: hoisted out of the K loop
+  // LDS reads are spread over the stage instead of issued in one burst at
+  // its start (all waves of the workgroup start a stage together after the
+  // barrier): B(0) and A(0) first, then A(i+1) one block ahead of its first
+  // use in the j = 0 row and B(j+1) one row ahead.
   f16x8 bcur[2], bnext[2];
   bcur[0] = read_b<C>(bs, wn, 0, 0, lane);
   bcur[1] = read_b<C>(bs, wn, 0, 1, lane);
-  f32x4 p0[2], p1[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) af[0][c] = read_kc<C>(as, wm * C::WTM + r16, 4 * c + g);
+  f32x4 p0[3], p1[3];
   f16x8 x[2];
 #pragma unroll
-  for (int t = 0; t < T + 2; ++t) {
+  for (int t = 0; t < T + 3; ++t) {
     const int i = t % C::FM, j = t / C::FM;
+    if (t < T && j == 0 && i + 1 < C::FM) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) af[i + 1][c] = read_kc<C>(as, wm * C::WTM + 16 * (i + 1) + r16, 4 * c + g);
+    }
     if (t < T && i == 0 && j + 1 < C::FN) {
       bnext[0] = read_b<C>(bs, wn, j + 1, 0, lane);
       bnext[1] = read_b<C>(bs, wn, j + 1, 1, lane);
     }
-    if (t < T) p0[t & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bcur[0], af[i][0], zero, 0, 0, 0);
-    if (t >= 1 && t <= T) x[(t - 1) & 1] = round_pair(p0[(t - 1) & 1], p1[(t - 1) & 1]);
-    if (t < T) p1[t & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bcur[1], af[i][1], zero, 0, 0, 0);
-    if (t >= 2) {
-      const int u = t - 2;
+    __builtin_amdgcn_sched_barrier(0);
+    if (t < T) p0[t % 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bcur[0], af[i][0], zero, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    const int q = t - 2;  // block rounded in this step
+    if (q >= 0 && q < T) round_half(p0[q % 3], p1[q % 3], x[q & 1], 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (t < T) p1[t % 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bcur[1], af[i][1], zero, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (q >= 0 && q < T) round_half(p0[q % 3], p1[q % 3], x[q & 1], 1);
+    __builtin_amdgcn_sched_barrier(0);
+    const int u = t - 3;  // block summed in this step
+    if (u >= 0) {
       acc[u % C::FM][u / C::FM] =
           __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, x[u & 1], acc[u % C::FM][u / C::FM], 0, 0, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);
     if (t < T && i == C::FM - 1 && j + 1 < C::FN) {
       bcur[0] = bnext[0];
       bcur[1] = bnext[1];
