@@ -222,18 +222,41 @@ struct FastLoader {
     }
   }
 
-  // Issue the global -> LDS copies of the stage starting at k = kbase.
-  __device__ void issue(const Params& p, int64_t m0, int64_t n0, int64_t kbase, int64_t kend, char LDS_AS* stage,
-                        int wave) {
+  // The copies of one stage (k from kbase): unit(j) issues this thread's
+  // j-th 16-byte copy, j < LA + LB (A units first).
+  struct Stage {
+    i32x4 ra, rb;
+    int lds, krem;
+    const FastLoader* ld;
+    __device__ __forceinline__ void unit(int j) const {
+      if (j < C::LA)
+        lds_dma16(ra, lds + j * C::T * 16, ld->a_k[j] < krem ? ld->a_off[j] : kOob);
+      else
+        lds_dma16(rb, lds + C::A_STAGE + (j - C::LA) * C::T * 16,
+                  ld->b_k[j - C::LA] < krem ? ld->b_off[j - C::LA] : kOob);
+    }
+    __device__ __forceinline__ void all() const {
+#pragma unroll
+      for (int j = 0; j < C::LA + C::LB; ++j) unit(j);
+    }
+  };
+
+  __device__ Stage stage(const Params& p, int64_t m0, int64_t n0, int64_t kbase, int64_t kend, char LDS_AS* slot,
+                         int wave) const {
+    Stage st;
     const int64_t krem = kend - kbase;  // k < krem is inside this workgroup's K range
-    const i32x4 ra = make_srd(p.a + (m0 * p.sam + kbase));
-    const i32x4 rb = C::BL == kKC ? make_srd(p.b + (n0 * p.sbn + kbase)) : make_srd(p.b + (kbase * p.sbk + n0));
-    const int lds = __builtin_amdgcn_readfirstlane((int)(uint32_t)(size_t)stage + wave * 64 * 16);
-#pragma unroll
-    for (int j = 0; j < C::LA; ++j) lds_dma16(ra, lds + j * C::T * 16, a_k[j] < krem ? a_off[j] : kOob);
-#pragma unroll
-    for (int j = 0; j < C::LB; ++j)
-      lds_dma16(rb, lds + C::A_STAGE + j * C::T * 16, b_k[j] < krem ? b_off[j] : kOob);
+    st.krem = krem < kStageK ? (int)krem : kStageK;
+    st.ra = make_srd(p.a + (m0 * p.sam + kbase));
+    st.rb = C::BL == kKC ? make_srd(p.b + (n0 * p.sbn + kbase)) : make_srd(p.b + (kbase * p.sbk + n0));
+    st.lds = __builtin_amdgcn_readfirstlane((int)(uint32_t)(size_t)slot + wave * 64 * 16);
+    st.ld = this;
+    return st;
+  }
+
+  // Issue all global -> LDS copies of the stage starting at k = kbase.
+  __device__ void issue(const Params& p, int64_t m0, int64_t n0, int64_t kbase, int64_t kend, char LDS_AS* slot,
+                        int wave) const {
+    stage(p, m0, n0, kbase, kend, slot, wave).all();
   }
 };
 
@@ -319,12 +342,14 @@ __device__ __forceinline__ f16x8 round_pair(const f32x4& p0, const f32x4& p1) {
 
 template <class C, bool CHUNKED>
 __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, int wn, int lane,
-                                              f32x4 (&acc)[C::FM][C::FN]) {
+                                              f32x4 (&acc)[C::FM][C::FN],
+                                              const typename FastLoader<C>::Stage& next, bool has_next) {
   const char LDS_AS* as = stage;
   const char LDS_AS* bs = stage + C::A_STAGE;
   const int r16 = lane & 15, g = lane >> 4;
   f16x8 af[C::FM][2];
   if (!CHUNKED) {
+    if (has_next) next.all();
 #pragma unroll
     for (int i = 0; i < C::FM; ++i)
 #pragma unroll
@@ -362,9 +387,19 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
   for (int c = 0; c < 2; ++c) af[0][c] = read_kc<C>(as, wm * C::WTM + r16, 4 * c + g);
   f32x4 p0[3], p1[3];
   f16x8 x[2];
+  // On the 256x256 tile the next stage's global -> LDS copies go out one at
+  // a time over the first half of the stage (every kDmaEvery steps) instead
+  // of in one burst that meets this stage's first fragment reads in the LDS
+  // (measured +1.5-2 %); the shorter 64x64-per-wave stages do better with
+  // the burst.
+  constexpr int kUnits = C::LA + C::LB;
+  constexpr bool kSpread = T >= 32;
+  constexpr int kDmaEvery = T / (2 * kUnits) > 0 ? T / (2 * kUnits) : 1;
+  if (!kSpread && has_next) next.all();
 #pragma unroll
   for (int t = 0; t < T + 3; ++t) {
     const int i = t % C::FM, j = t / C::FM;
+    if (kSpread && has_next && t % kDmaEvery == 0 && t / kDmaEvery < kUnits) next.unit(t / kDmaEvery);
     if (t < T && j == 0 && i + 1 < C::FM) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) af[i + 1][c] = read_kc<C>(as, wm * C::WTM + 16 * (i + 1) + r16, 4 * c + g);
@@ -419,11 +454,9 @@ __device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t
       wait_vm0();
     __syncthreads();
     const int64_t nxt = s + C::NS - 1;
-    if (nxt < nsteps) {
-      const int nslot = slot == 0 ? C::NS - 1 : slot - 1;  // (s + NS - 1) % NS
-      ld.issue(p, m0, n0, kbeg + nxt * kStageK, kend, smem + nslot * C::STAGE, wave);
-    }
-    compute_stage<C, CHUNKED>(smem + slot * C::STAGE, wm, wn, lane, acc);
+    const int nslot = slot == 0 ? C::NS - 1 : slot - 1;  // (s + NS - 1) % NS
+    const typename FastLoader<C>::Stage next = ld.stage(p, m0, n0, kbeg + nxt * kStageK, kend, smem + nslot * C::STAGE, wave);
+    compute_stage<C, CHUNKED>(smem + slot * C::STAGE, wm, wn, lane, acc, next, nxt < nsteps);
     slot = slot + 1 == C::NS ? 0 : slot + 1;
   }
   __syncthreads();  // LDS free for a redo pass
@@ -467,7 +500,8 @@ __device__ __forceinline__ void k_loop_generic(const Params& p, int64_t m0, int6
   for (int64_t s = 0; s < nsteps; ++s) {
     stage_generic<C>(p, m0, n0, s * kStageK, smem, tid);
     __syncthreads();
-    compute_stage<C, CHUNKED>(smem, wm, wn, lane, acc);
+    const typename FastLoader<C>::Stage none{};
+    compute_stage<C, CHUNKED>(smem, wm, wn, lane, acc, none, false);
     __syncthreads();
   }
 }
