@@ -518,6 +518,48 @@ __device__ __forceinline__ float with_bias(float v, const f16* bias, int64_t col
   return OUT32 ? v + b : (float)(f16)v + b;
 }
 
+// fp16 output of a tile that lies wholly inside c, staged through LDS so
+// that every lane stores 16 contiguous bytes and a row leaves as whole cache
+// lines: the MFMA layout alone gives 8-byte stores covering 32 bytes of a
+// row per instruction, which reached HBM as partial lines (about twice the
+// output's bytes written, by rocprofv3 WRITE_SIZE).  Each wave stages its
+// own WTM x WTN sub-tile in its own LDS slice (the LDS is free once the K
+// loop's final barrier has passed), 16-byte units XOR-swizzled by row.
+template <class C>
+__device__ __forceinline__ void store_tile_staged(const Params& p, int64_t m0, int64_t n0, int wm, int wn, int lane,
+                                                  int wave, char LDS_AS* smem, const f32x4 (&acc)[C::FM][C::FN]) {
+  typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+  constexpr int U = C::WTN / 8;  // 16-byte units per row of the wave tile
+  constexpr int ROW = C::WTN * 2;
+  char LDS_AS* w = smem + wave * (C::WTM * ROW);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int64_t col0 = n0 + wn * C::WTN;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) {
+      const int row = 16 * i + r16, u = 2 * j + (g >> 1);
+      f32x4 v = acc[i][j];
+      if (p.bias) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = with_bias<false>(v[r], p.bias, col0 + 16 * j + 4 * g + r);
+      }
+      const f32x2 lo = {v[0], v[1]}, hi = {v[2], v[3]};
+      const f16x2 hl = __builtin_convertvector(lo, f16x2), hh = __builtin_convertvector(hi, f16x2);
+      const f16x4 o = {hl[0], hl[1], hh[0], hh[1]};
+      *(f16x4 LDS_AS*)(w + row * ROW + ((u ^ (row % U)) << 4) + (g & 1) * 8) = o;
+    }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
+  __builtin_amdgcn_wave_barrier();
+  f16* cbase = (f16*)p.c + (m0 + wm * C::WTM) * p.scm + col0;
+#pragma unroll
+  for (int it = 0; it < C::WTM * U / 64; ++it) {
+    const int idx = it * 64 + lane, row = idx / U, u = idx % U;
+    const f16x8 v = *(const f16x8 LDS_AS*)(w + row * ROW + ((u ^ (row % U)) << 4));
+    *(f16x8*)(cbase + row * p.scm + 8 * u) = v;
+  }
+}
+
 template <class C, bool OUT32>
 __device__ __forceinline__ void store_tile(const Params& p, int64_t m0, int64_t n0, int wm, int wn, int lane,
                                            const f32x4 (&acc)[C::FM][C::FN]) {
@@ -562,7 +604,7 @@ __device__ __forceinline__ void store_tile(const Params& p, int64_t m0, int64_t 
 
 // Flag, redo and store of a finished FP32 tile sum (shared by the whole-K
 // kernel and the split-K finishing kernel).
-template <class C, bool FAST, bool CHUNKED, bool OUT32>
+template <class C, bool FAST, bool CHUNKED, bool OUT32, int SMEM>
 __device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, FastLoader<C>& ld, int* tile_bad,
                                             int64_t tm, int64_t tn, int tid, int wave, int wm, int wn, int lane,
                                             f32x4 (&acc)[C::FM][C::FN]) {
@@ -592,7 +634,10 @@ __device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, 
         k_loop_generic<C, false>(p, m0, n0, smem, tid, wm, wn, lane, acc);
     }
   }
-  store_tile<C, OUT32>(p, m0, n0, wm, wn, lane, acc);
+  if (!OUT32 && C::BM * C::BN * 2 <= SMEM && p.vec_store && m0 + C::BM <= p.M && n0 + C::BN <= p.N)
+    store_tile_staged<C>(p, m0, n0, wm, wn, lane, wave, smem, acc);
+  else
+    store_tile<C, OUT32>(p, m0, n0, wm, wn, lane, acc);
 }
 
 // FP32 partials of a split tile, thread-private order: split s, block
@@ -661,7 +706,8 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void 
                                                part_offset<C>(i, j, 0) * 4, 0);
     return;
   }
-  finish_tile<C, FAST, CHUNKED, OUT32>(p, smem, ld, &tile_bad, tm, tn, tid, wave, wm, wn, lane, acc);
+  finish_tile<C, FAST, CHUNKED, OUT32, (FAST ? C::NS * C::STAGE : C::STAGE)>(p, smem, ld, &tile_bad, tm, tn, tid,
+                                                                            wave, wm, wn, lane, acc);
 }
 
 // Split-K finishing kernel (kFinish): one workgroup per tile adds the FP32
@@ -671,7 +717,8 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void 
 // generic strided path, so C is the K-contiguous variant of the tile shape.
 template <class C, bool CHUNKED, bool OUT32>
 __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void finish_kernel(Params p) {
-  __shared__ __attribute__((aligned(1024))) char smem_raw[C::STAGE];
+  constexpr int kSmem = C::STAGE > C::BM * C::BN * 2 ? C::STAGE : C::BM * C::BN * 2;
+  __shared__ __attribute__((aligned(1024))) char smem_raw[kSmem];
   __shared__ int tile_bad;
   char LDS_AS* smem = (char LDS_AS*)smem_raw;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -695,7 +742,7 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void 
       for (int j = 0; j < C::FN; ++j) acc[i][j] += *(const f32x4*)(ps + part_offset<C>(i, j, tid));
   }
   FastLoader<C> unused;
-  finish_tile<C, false, CHUNKED, OUT32>(p, smem, unused, &tile_bad, tm, tn, tid, wave, wm, wn, lane, acc);
+  finish_tile<C, false, CHUNKED, OUT32, kSmem>(p, smem, unused, &tile_bad, tm, tn, tid, wave, wm, wn, lane, acc);
 }
 
 // ---------------------------------------------------------------------------
