@@ -340,10 +340,59 @@ __device__ __forceinline__ f16x8 round_pair(const f32x4& p0, const f32x4& p1) {
   return x;
 }
 
+// State of the chunk pipeline carried from one stage into the next, so the
+// pipeline does not drain at every stage boundary: the FP32 partials of the
+// last blocks (ring of 4, indexed by block % 4; a stage's block count is a
+// multiple of 4, so ring slots line up across stages) and their rounded
+// pairs (ring of 2).  It starts all zero, so the first stage's carry steps
+// round zeros and add them to accumulators that are still zero: no branch.
+template <class C>
+struct Pipe {
+  f32x4 p0[4], p1[4];
+  f16x8 x[2];
+  __device__ __forceinline__ Pipe() {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p0[r] = p1[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    x[0] = x[1] = f16x8{};
+  }
+};
+
+// Rounding of block q and selector sum of block u of the pipeline; negative
+// indices name the previous stage's last blocks (q + T, u + T).
+template <class C>
+__device__ __forceinline__ void pipe_round(Pipe<C>& pp, int q, int h) {
+  constexpr int T = C::FM * C::FN;
+  const int b = q < 0 ? q + T : q;
+  round_half(pp.p0[b % 4], pp.p1[b % 4], pp.x[b & 1], h);
+}
+
+template <class C>
+__device__ __forceinline__ void pipe_sum(Pipe<C>& pp, const f16x8& sel, int u, f32x4 (&acc)[C::FM][C::FN]) {
+  constexpr int T = C::FM * C::FN;
+  const int b = u < 0 ? u + T : u;
+  acc[b % C::FM][b / C::FM] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, pp.x[b & 1], acc[b % C::FM][b / C::FM], 0, 0, 0);
+}
+
+// The pending work the last stage leaves: rounds of its blocks T-2, T-1 and
+// sums of T-3, T-2, T-1.
+template <class C>
+__device__ __forceinline__ void pipe_drain(Pipe<C>& pp, int lane, f32x4 (&acc)[C::FM][C::FN]) {
+  const f16x8 sel = chunk_pair_selector(lane);
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    if (t < 2) {
+      pipe_round<C>(pp, t - 2, 0);
+      pipe_round<C>(pp, t - 2, 1);
+    }
+    pipe_sum<C>(pp, sel, t - 3, acc);
+  }
+}
+
 template <class C, bool CHUNKED>
 __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, int wn, int lane,
                                               f32x4 (&acc)[C::FM][C::FN],
-                                              const typename FastLoader<C>::Stage& next, bool has_next) {
+                                              const typename FastLoader<C>::Stage& next, bool has_next,
+                                              Pipe<C>& pp) {
   const char LDS_AS* as = stage;
   const char LDS_AS* bs = stage + C::A_STAGE;
   const int r16 = lane & 15, g = lane >> 4;
@@ -370,9 +419,12 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
   // pipelined four deep.  Step t issues block t's two chunk MFMAs with the
   // rounding of block t-2 between them (half after each), then the selector
   // MFMA of block t-3: every instruction reads an MFMA result at least three
-  // MFMAs old, so nothing waits on the matrix pipe.  sched_barrier fences keep
-  // that order (left to itself the scheduler puts each conversion right
-  // behind the MFMA that produces its input and pads with s_nop).
+  // MFMAs old, so nothing waits on the matrix pipe.  The first steps of a
+  // stage finish the previous stage's last blocks (carry), so the pipeline
+  // only drains once, after the K loop.  sched_barrier fences keep that
+  // order (left to itself the scheduler puts each conversion right behind
+  // the MFMA that produces its input and pads with s_nop).
+  static_assert(C::FM * C::FN % 4 == 0, "block count must be a multiple of the partials ring");
   constexpr int T = C::FM * C::FN;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   const f16x8 sel = chunk_pair_selector(lane);  // loop invariant: hoisted out of the K loop
@@ -385,8 +437,6 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
   bcur[1] = read_b<C>(bs, wn, 0, 1, lane);
 #pragma unroll
   for (int c = 0; c < 2; ++c) af[0][c] = read_kc<C>(as, wm * C::WTM + r16, 4 * c + g);
-  f32x4 p0[3], p1[3];
-  f16x8 x[2];
   // On the 256x256 tile the next stage's global -> LDS copies go out one at
   // a time over the first half of the stage (every kDmaEvery steps) instead
   // of in one burst that meets this stage's first fragment reads in the LDS
@@ -397,34 +447,29 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
   constexpr int kDmaEvery = T / (2 * kUnits) > 0 ? T / (2 * kUnits) : 1;
   if (!kSpread && has_next) next.all();
 #pragma unroll
-  for (int t = 0; t < T + 3; ++t) {
+  for (int t = 0; t < T; ++t) {
     const int i = t % C::FM, j = t / C::FM;
     if (kSpread && has_next && t % kDmaEvery == 0 && t / kDmaEvery < kUnits) next.unit(t / kDmaEvery);
-    if (t < T && j == 0 && i + 1 < C::FM) {
+    if (j == 0 && i + 1 < C::FM) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) af[i + 1][c] = read_kc<C>(as, wm * C::WTM + 16 * (i + 1) + r16, 4 * c + g);
     }
-    if (t < T && i == 0 && j + 1 < C::FN) {
+    if (i == 0 && j + 1 < C::FN) {
       bnext[0] = read_b<C>(bs, wn, j + 1, 0, lane);
       bnext[1] = read_b<C>(bs, wn, j + 1, 1, lane);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (t < T) p0[t % 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bcur[0], af[i][0], zero, 0, 0, 0);
+    pp.p0[t % 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bcur[0], af[i][0], zero, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    const int q = t - 2;  // block rounded in this step
-    if (q >= 0 && q < T) round_half(p0[q % 3], p1[q % 3], x[q & 1], 0);
+    pipe_round<C>(pp, t - 2, 0);
     __builtin_amdgcn_sched_barrier(0);
-    if (t < T) p1[t % 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bcur[1], af[i][1], zero, 0, 0, 0);
+    pp.p1[t % 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bcur[1], af[i][1], zero, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    if (q >= 0 && q < T) round_half(p0[q % 3], p1[q % 3], x[q & 1], 1);
+    pipe_round<C>(pp, t - 2, 1);
     __builtin_amdgcn_sched_barrier(0);
-    const int u = t - 3;  // block summed in this step
-    if (u >= 0) {
-      acc[u % C::FM][u / C::FM] =
-          __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, x[u & 1], acc[u % C::FM][u / C::FM], 0, 0, 0);
-    }
+    pipe_sum<C>(pp, sel, t - 3, acc);
     __builtin_amdgcn_sched_barrier(0);
-    if (t < T && i == C::FM - 1 && j + 1 < C::FN) {
+    if (i == C::FM - 1 && j + 1 < C::FN) {
       bcur[0] = bnext[0];
       bcur[1] = bnext[1];
     }
@@ -447,6 +492,7 @@ __device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t
   for (int s0 = 0; s0 < C::NS - 1; ++s0)
     if (s0 < nsteps) ld.issue(p, m0, n0, kbeg + (int64_t)s0 * kStageK, kend, smem + s0 * C::STAGE, wave);
   int slot = 0;
+  Pipe<C> pp;
   for (int64_t s = 0; s < nsteps; ++s) {
     if (s + C::NS - 2 < nsteps)
       wait_vm<(C::NS - 2) * (C::LA + C::LB)>();
@@ -456,9 +502,10 @@ __device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t
     const int64_t nxt = s + C::NS - 1;
     const int nslot = slot == 0 ? C::NS - 1 : slot - 1;  // (s + NS - 1) % NS
     const typename FastLoader<C>::Stage next = ld.stage(p, m0, n0, kbeg + nxt * kStageK, kend, smem + nslot * C::STAGE, wave);
-    compute_stage<C, CHUNKED>(smem + slot * C::STAGE, wm, wn, lane, acc, next, nxt < nsteps);
+    compute_stage<C, CHUNKED>(smem + slot * C::STAGE, wm, wn, lane, acc, next, nxt < nsteps, pp);
     slot = slot + 1 == C::NS ? 0 : slot + 1;
   }
+  if (CHUNKED && nsteps > 0) pipe_drain<C>(pp, lane, acc);
   __syncthreads();  // LDS free for a redo pass
 }
 
@@ -497,13 +544,15 @@ template <class C, bool CHUNKED>
 __device__ __forceinline__ void k_loop_generic(const Params& p, int64_t m0, int64_t n0, char LDS_AS* smem,
                                                int tid, int wm, int wn, int lane, f32x4 (&acc)[C::FM][C::FN]) {
   const int64_t nsteps = (p.K + kStageK - 1) / kStageK;
+  Pipe<C> pp;
   for (int64_t s = 0; s < nsteps; ++s) {
     stage_generic<C>(p, m0, n0, s * kStageK, smem, tid);
     __syncthreads();
     const typename FastLoader<C>::Stage none{};
-    compute_stage<C, CHUNKED>(smem, wm, wn, lane, acc, none, false);
+    compute_stage<C, CHUNKED>(smem, wm, wn, lane, acc, none, false, pp);
     __syncthreads();
   }
+  if (CHUNKED && nsteps > 0) pipe_drain<C>(pp, lane, acc);
 }
 
 // Output value of one element.  With a bias the epilogue reproduces the
