@@ -2,7 +2,9 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
 
-A step is one f16acc_amd.mm call on inputs already resident in HBM.  The
+A step is one f16acc_amd.mm call on inputs already resident in HBM.  Each
+timed op first runs back to back for 0.2 s so the GPU clock has settled, then
+W warm-up steps, then exactly K timed steps.  The
 default workload is the headline one: M = N = K = 4096, A and B ~ N(0, 1)
 cast to fp16, B row-major [K, N] (as the reference's bench/gemm_bench.py
 passes it), fp16 output, chunk-32 with FP32 chunk sum and in-kernel overflow
@@ -34,6 +36,7 @@ sys.path.insert(0, ROOT)
 PEAK_TFLOPS = 2516.6  # MI355X dense fp16 MFMA: 256 CU x 2.4 GHz x 4096 flop/clk
 METRIC = "TFLOPS at 4096³ fp16 GEMM (1 GPU, % of fp16 MFMA peak); max rel err vs FP64"
 REF_TFLOPS = 65.7  # reference README.md:29, RTX 4060 Ti, same GEMM (fp16 out)
+PREHEAT_S = 0.2  # seconds of back-to-back calls before the warm-up steps
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_4096_fp16out_rowmajorB_traffic.txt")
 
 WORKLOADS = {
@@ -67,9 +70,25 @@ def make_inputs(M, N, K, layout, seed=0, device="cuda"):
     return a, b, a.to(device), gb
 
 
+def preheat(op, seconds=None):
+    """Run `op` back to back for about `seconds` of wall time.  From idle the
+    MI355X's shader clock dips a few milliseconds into a load and takes
+    ~15 ms to settle again (a 4096^3 GEMM: ~152 us per call, ~205 us in the
+    dip): a window timed straight after a short warm-up measures that
+    transient, for this kernel and hipBLASLt alike."""
+    seconds = PREHEAT_S if seconds is None else seconds
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            op()
+        torch.cuda.synchronize()
+
+
 def time_steps(op, steps, warmup):
-    """Warm up, then time exactly `steps` calls between two synchronisations.
-    Returns (total seconds, event seconds on the current stream)."""
+    """Pre-heat the clock, warm up, then time exactly `steps` calls between two
+    synchronisations.  Returns (total seconds, event seconds on the current
+    stream)."""
+    preheat(op)
     for _ in range(warmup):
         op()
     torch.cuda.synchronize()
@@ -82,21 +101,6 @@ def time_steps(op, steps, warmup):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return wall, start.elapsed_time(stop) / 1e3
-
-
-def median_event_time(op, iters=30, warmup=10):
-    for _ in range(warmup):
-        op()
-    torch.cuda.synchronize()
-    vals = []
-    for _ in range(iters):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        op()
-        e.record()
-        torch.cuda.synchronize()
-        vals.append(s.elapsed_time(e) / 1e3)
-    return statistics.median(vals)
 
 
 def read_traffic():
@@ -322,15 +326,19 @@ def copy_reference(steps, warmup, nbytes=1 << 30):
 
 
 def main():
+    global PREHEAT_S
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="gemm4096", choices=sorted(WORKLOADS) + ["copy", "overflow", "qwen2_prefill"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and oracle comparison")
+    ap.add_argument("--preheat", type=float, default=PREHEAT_S,
+                    help="seconds of back-to-back calls before the warm-up steps (0 for counter runs)")
     ap.add_argument("--sweep-tiles", nargs="*", metavar="WORKLOAD",
                     help="time every tile configuration on these workloads (all if none given) and exit")
     args = ap.parse_args()
+    PREHEAT_S = args.preheat
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: there is no multi-GPU path (a GEMM would shard by M or N "
               "tiles with no exchange, or by K in multiples of 32 with one FP32 all-reduce); "
@@ -369,8 +377,10 @@ def main():
     err_fp64 = ((c.double() - ref64).abs().max() / ref64.abs().max()).item()
     del ref64
 
-    blas_t = median_event_time(lambda: torch.mm(a, b) if out_dtype == torch.float16 else torch.mm(a, b).float())
-    fp32acc_t = median_event_time(lambda: f16acc_amd.mm(a, b, out_dtype, chunked=False))
+    # the comparisons run like the measured op: pre-heated, back to back
+    blas_op = (lambda: torch.mm(a, b)) if out_dtype == torch.float16 else (lambda: torch.mm(a, b).float())
+    blas_t = time_steps(blas_op, args.steps, args.warmup)[1] / args.steps
+    fp32acc_t = time_steps(lambda: f16acc_amd.mm(a, b, out_dtype, chunked=False), args.steps, args.warmup)[1] / args.steps
 
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": args.steps,
