@@ -65,7 +65,7 @@ ABI_VERSION = 2
 
 OUT_F16, OUT_F32 = 0, 1
 E_ARG, E_UNSUPPORTED = -1, -2
-TILES = ("256x256", "256x128", "128x256", "128x128", "generic")  # F16ACC_TILE_* ids
+TILES = ("256x256", "256x128", "128x256", "128x128", "generic", "64x64")  # F16ACC_TILE_* ids
 TILE_GENERIC = 4
 
 if abi_version() != ABI_VERSION:

@@ -139,7 +139,9 @@ struct Cfg {
   static constexpr int UB = BN / 8;                              // NC: units per k-row
   static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave tile must be whole 16x16 blocks");
   static_assert(BM * 8 % T == 0 && BN * 8 % T == 0, "stage must split evenly over threads");
-  static_assert(BL == kKC || BN >= 128, "NC swizzle needs at least 16 units per k-row");
+  // The NC swizzle spreads a k-row over 16 units; at BN = 64 (8 units) it
+  // folds onto 8 (still a permutation, some transpose reads then conflict).
+  static_assert(BL == kKC || BN >= 64, "NC k-rows need at least 8 units");
   static_assert(NS >= 2 && NS * STAGE <= 160 * 1024, "LDS ring must fit the 160 KiB of a CU");
   // Split-K partial stores are compiled only into tiles of 64x64 per wave:
   // at 64x128 per wave the chunked kernel already uses ~240 of its 256
@@ -835,17 +837,20 @@ __global__ __launch_bounds__(256) void pack_kernel(const f16* __restrict__ src, 
 //   2   128x256  8      64x64      3 x 48 KiB    1
 //   3   128x128  4      64x64      2 x 32 KiB    2
 //   4   128x128  4      64x64      1 x 32 KiB    generic strided gather path
+//   5   64x64    4      32x32      3 x 16 KiB    3
 template <int BL> using Cfg0 = Cfg<256, 256, 4, 2, 2, BL>;
 template <int BL> using Cfg1 = Cfg<256, 128, 4, 2, 3, BL>;
 template <int BL> using Cfg2 = Cfg<128, 256, 2, 4, 3, BL>;
 template <int BL> using Cfg3 = Cfg<128, 128, 2, 2, 2, BL>;
+template <int BL> using Cfg5 = Cfg<64, 64, 2, 2, 3, BL>;
 using CfgG = Cfg<128, 128, 2, 2, 2, kKC>;
 
 struct TileInfo {
   int bm, bn, threads, per_cu;
 };
 constexpr TileInfo kTiles[F16ACC_NUM_TILES] = {
-    {256, 256, 512, 1}, {256, 128, 512, 1}, {128, 256, 512, 1}, {128, 128, 256, 2}, {128, 128, 256, 2}};
+    {256, 256, 512, 1}, {256, 128, 512, 1}, {128, 256, 512, 1}, {128, 128, 256, 2}, {128, 128, 256, 2},
+    {64, 64, 256, 3}};
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -883,7 +888,20 @@ constexpr double kTileRate[4] = {1.00, 0.87, 0.87, 0.89};
 
 // The per-shape table: the fast tile with the smallest estimated time.
 // Ties keep the larger tile.
-inline int choose_tile(int64_t M, int64_t N, int cus) {
+//
+// Small grids: when the pick leaves workgroup slots empty and K is too short
+// for a split (fewer than 2 x kMinSplitStages stages), the 64x64 tile is
+// weighed against it by rounds of full-occupancy workgroups:
+//   estimated time = ceil(tiles / (CUs x per_cu)) x tile area x per_cu / rate
+// (64x64 runs three workgroups per CU, each wave 32x32: it reads twice the
+// LDS per MFMA of a 64x64 wave tile, rate 0.65, but four times the tiles
+// fill the GPU: Qwen2.5-1.5B k/v 2048x256x1536 20.0 -> 11.3 us, q/o
+// 2048x1536x1536 21.6 -> 19.7 us; gate/up 2048x8960x1536 stays on 128x128,
+// 83.6 us against 101 us).
+constexpr double kSmallTileRate = 0.65;
+constexpr int kMinSplitStages = 16;
+
+inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus) {
   int best = 0;
   double best_t = 0;
   for (int id = 0; id < 4; ++id) {
@@ -895,6 +913,16 @@ inline int choose_tile(int64_t M, int64_t N, int cus) {
       best_t = est;
     }
   }
+  const TileInfo& t = kTiles[best];
+  const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn), slots = (int64_t)cus * t.per_cu;
+  if (tiles < slots && cdiv(K, kStageK) < 2 * kMinSplitStages) {
+    const TileInfo& s = kTiles[F16ACC_TILE_64x64];
+    const int64_t stiles = cdiv(M, s.bm) * cdiv(N, s.bn);
+    const double est_best = (double)t.bm * t.bn * t.per_cu / kTileRate[best];
+    const double est_small =
+        (double)cdiv(stiles, (int64_t)cus * s.per_cu) * s.bm * s.bn * s.per_cu / kSmallTileRate;
+    if (est_small < est_best * 0.999) return F16ACC_TILE_64x64;
+  }
   return best;
 }
 
@@ -904,7 +932,7 @@ struct Choice {
 
 inline Choice choose(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
                      const void* a, const void* b, int forced_tile) {
-  const int id = forced_tile >= 0 ? forced_tile : choose_tile(M, N, cu_count());
+  const int id = forced_tile >= 0 ? forced_tile : choose_tile(M, N, K, cu_count());
   if (id == F16ACC_TILE_GENERIC) return Choice{id, F16ACC_FAMILY_GENERIC, kKC};
   const int bl = fast_layout(N, K, sam, sak, sbk, sbn, a, b, kTiles[id].bm, kTiles[id].bn);
   if (bl < 0) return Choice{F16ACC_TILE_GENERIC, F16ACC_FAMILY_GENERIC, kKC};
@@ -958,7 +986,6 @@ hipError_t launch_finish(const Params& p, int out32, int chunked, hipStream_t st
 // Qwen2.5 down projection, K = 8960, gains; K = 1536 loses), so each split
 // keeps at least kMinSplitStages LDS stages; at most kMaxSplits.
 constexpr int kMaxSplits = 16;
-constexpr int kMinSplitStages = 16;
 
 struct SplitPlan {
   int splits;
@@ -968,7 +995,8 @@ struct SplitPlan {
 
 inline SplitPlan plan_split(const Choice& ch, int64_t M, int64_t N, int64_t K, int cus) {
   SplitPlan sp{1, K, 0};
-  if (ch.family != F16ACC_FAMILY_FAST || ch.tile == F16ACC_TILE_256x256) return sp;  // not SPLITTABLE
+  // 256x256 is not SPLITTABLE; 64x64 is only chosen where K is too short to split
+  if (ch.family != F16ACC_FAMILY_FAST || ch.tile == F16ACC_TILE_256x256 || ch.tile == F16ACC_TILE_64x64) return sp;
   const TileInfo& t = kTiles[ch.tile];
   const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
   const int64_t slots = (int64_t)cus * t.per_cu;
@@ -1030,13 +1058,14 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
       case 1: return (int)launch_fast<Cfg1>(q, ch.blayout, out32, chunked, st);
       case 2: return (int)launch_fast<Cfg2>(q, ch.blayout, out32, chunked, st);
       case 3: return (int)launch_fast<Cfg3>(q, ch.blayout, out32, chunked, st);
+      case 5: return (int)launch_fast<Cfg5>(q, ch.blayout, out32, chunked, st);
       default: return (int)launch_cfg<CfgG, false>(q, out32, chunked, st);
     }
   };
   int rc = launch(p);
   if (rc != 0 || p.mode != kPartial) return rc;
   p.mode = kFinish;
-  switch (ch.tile) {  // 256x256 never splits (plan_split)
+  switch (ch.tile) {  // 256x256 and 64x64 never split (plan_split)
     case 1: return (int)launch_finish<Cfg1>(p, out32, chunked, st);
     case 2: return (int)launch_finish<Cfg2>(p, out32, chunked, st);
     default: return (int)launch_finish<Cfg3>(p, out32, chunked, st);

@@ -127,22 +127,30 @@ def _pack(src, rows, cols, s_r, s_c, ld):
     return dst
 
 
-def _operands(a, b, M, N, K, tile=None):
-    """The operands the GEMM runs on: a and b themselves when the fast kernels
-    can read them (or the problem is too small to repay a copy, or the
-    generic tile is forced), else packed copies with K padded to a multiple
-    of 8 by zeros: a as [M, Kp] rows, b as the K-contiguous [Kp, N] view of an
-    [N, Kp] buffer.  Returns (a, b, K) for the launch."""
+def _pack_plan(a, b, M, N, K, tile=None):
+    """(pack_a, pack_b, Kp): which operands mm copies before the GEMM, and the
+    K it then runs with.  Nothing is packed when the fast kernels can read a
+    and b directly, when the problem is too small to repay a copy, or when the
+    generic tile is forced; otherwise K is padded to a multiple of 8 by zeros
+    and every operand that is not fast (or all, when K changes) is packed."""
     if K == 0 or tile == "generic" or (tile is None and M * N * K < PACK_MIN_MACS):
-        return a, b, K
+        return False, False, K
     ok_a, ok_b = _fast_a(a, K), _fast_b(b, K, N)
     if ok_a and ok_b:
-        return a, b, K
+        return False, False, K
     Kp = -(-K // 8) * 8
-    if Kp != K or not ok_a:
+    return Kp != K or not ok_a, Kp != K or not ok_b, Kp
+
+
+def _operands(a, b, M, N, K, tile=None):
+    """The operands the GEMM runs on (see _pack_plan): a as [M, Kp] rows, b as
+    the K-contiguous [Kp, N] view of an [N, Kp] buffer when packed.
+    Returns (a, b, K) for the launch."""
+    pack_a, pack_b, Kp = _pack_plan(a, b, M, N, K, tile)
+    if pack_a:
         with torch.cuda.device(a.device):
             a = _pack(a, M, K, a.stride(0), a.stride(1), Kp)
-    if Kp != K or not ok_b:
+    if pack_b:
         with torch.cuda.device(b.device):
             b = _pack(b, N, K, b.stride(1), b.stride(0), Kp).t()  # element (n, k) = b[k][n]
     return a, b, Kp
@@ -189,17 +197,21 @@ def _tile_id(tile):
 
 
 def tile_config(a, b, tile=None):
-    """The per-shape tile choice the library makes for a @ b (replaces the
-    reference's autotuned best_config, kernel.py:16-19, 101-102), or what a
-    forced `tile` resolves to for these operands."""
+    """The tile configuration mm uses for a @ b (replaces the reference's
+    autotuned best_config, kernel.py:16-19, 101-102), or what a forced `tile`
+    resolves to, for the operands the GEMM actually reads: when mm would pack
+    a or b first, the packed copies' layout (contiguous, 16-byte aligned rows
+    of Kp elements)."""
     M, K = a.shape
     N = b.shape[1]
+    pack_a, pack_b, Kp = _pack_plan(a, b, M, N, K, tile) if M and N else (False, False, K)
+    sam, sak, pa = (Kp, 1, 0) if pack_a else (a.stride(0), a.stride(1), a.data_ptr())
+    sbk, sbn, pb = (1, Kp, 0) if pack_b else (b.stride(0), b.stride(1), b.data_ptr())
     tid, bm, bn, fam, thr = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     tm, tn = ctypes.c_int64(), ctypes.c_int64()
-    _lib.check(_lib.tile_config(M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
-                                a.data_ptr(), b.data_ptr(), _tile_id(tile), ctypes.byref(tid), ctypes.byref(bm),
-                                ctypes.byref(bn), ctypes.byref(tm), ctypes.byref(tn), ctypes.byref(fam),
-                                ctypes.byref(thr)))
+    _lib.check(_lib.tile_config(M, N, Kp, sam, sak, sbk, sbn, pa, pb, _tile_id(tile), ctypes.byref(tid),
+                                ctypes.byref(bm), ctypes.byref(bn), ctypes.byref(tm), ctypes.byref(tn),
+                                ctypes.byref(fam), ctypes.byref(thr)))
     return {"tile": _lib.TILES[tid.value], "bm": bm.value, "bn": bn.value, "tiles_m": tm.value,
             "tiles_n": tn.value, "family": ("fast", "generic")[fam.value], "threads": thr.value}
 

@@ -107,8 +107,13 @@ class _Fake:
     (8192, 8192, 8192, (8192, 1), (8192, 1), "fast", "256x256"),
     (2048, 151936, 1536, (1536, 1), (1, 1536), "fast", "256x256"),  # lm_head
     (2048, 8960, 1536, (1536, 1), (1, 1536), "fast", "128x128"),   # 280 256-tiles: ragged 2nd wave
-    (2048, 1536, 1536, (1536, 1), (1, 1536), "fast", "128x128"),   # too few 256-tiles to fill the CUs
-    (2049, 1537, 8961, (8961, 1), (1, 8961), "generic", "generic"),  # rows not 16-byte aligned
+    (2048, 1536, 1536, (1536, 1), (1, 1536), "fast", "64x64"),     # 192 128-tiles for 512 slots, K short
+    (2048, 256, 1536, (1536, 1), (1, 1536), "fast", "64x64"),      # Qwen k/v: 32 128-tiles
+    (2048, 1536, 8960, (8960, 1), (1, 8960), "fast", "128x128"),   # few tiles but K long: split-K instead
+    (128, 1536, 1536, (1536, 1), (1536, 1), "fast", "64x64"),      # 128 rows, row-major b
+    (2049, 1537, 8961, (8961, 1), (1, 8961), "fast", "128x128"),   # rows not 16-byte aligned: packed first
+    (300, 1537, 8961, (8961, 1), (1, 8961), "fast", "128x128"),    # packed; K long enough to split
+    (64, 40, 24, (24, 1), (40, 1), "fast", "64x64"),               # too small to repay a copy: as given
     (300, 200, 256, (512, 2), (700, 3), "generic", "generic"),      # strided operands
 ])
 def test_tile_table(M, N, K, sa, sb, fam, tile):
@@ -117,21 +122,35 @@ def test_tile_table(M, N, K, sa, sb, fam, tile):
     assert cfg["tiles_m"] == -(-M // cfg["bm"]) and cfg["tiles_n"] == -(-N // cfg["bn"])
 
 
-@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic"])
+@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic", "64x64"])
 def test_forced_tile_resolves(tile):
     bm, bn = (128, 128) if tile == "generic" else map(int, tile.split("x"))
     cfg = tile_config(_Fake((4096, 1024), (1024, 1)), _Fake((1024, 2048), (2048, 1)), tile)
     assert cfg["tile"] == tile and (cfg["bm"], cfg["bn"]) == (bm, bn)
     assert cfg["family"] == ("generic" if tile == "generic" else "fast")
-    # strided operands cannot take a fast tile: the forced choice falls back
+    # strided operands: mm packs them for a forced fast tile, so the tile holds
     cfg = tile_config(_Fake((300, 256), (512, 2)), _Fake((256, 200), (700, 3)), tile)
-    assert cfg["tile"] == "generic"
+    assert cfg["tile"] == tile
+    # the library itself, handed operands it cannot copy 16 bytes at a time,
+    # falls back to the generic kernel
+    tid = ctypes.c_int()
+    _lib.check(_lib.tile_config(300, 200, 256, 512, 2, 700, 3, 0, 0, _lib.TILES.index(tile), ctypes.byref(tid),
+                                None, None, None, None, None, None))
+    assert _lib.TILES[tid.value] == "generic"
     with pytest.raises(ValueError):
-        tile_config(_Fake((4096, 1024), (1024, 1)), _Fake((1024, 2048), (2048, 1)), "64x64")
+        tile_config(_Fake((4096, 1024), (1024, 1)), _Fake((1024, 2048), (2048, 1)), "32x32")
 
 
-def test_misaligned_pointer_takes_the_generic_path():
+def test_misaligned_pointer_is_packed_or_gathered():
+    # mm copies a misaligned operand into an aligned buffer when the GEMM is
+    # big enough to repay it; the library, handed the pointer itself, gathers
     cfg = tile_config(_Fake((4096, 4096), (4096, 1), ptr=4098), _Fake((4096, 4096), (4096, 1)))
+    assert cfg["family"] == "fast"
+    fam = ctypes.c_int()
+    _lib.check(_lib.tile_config(4096, 4096, 4096, 4096, 1, 4096, 1, 4098, 0, -1, None, None, None, None, None,
+                                ctypes.byref(fam), None))
+    assert fam.value == 1  # F16ACC_FAMILY_GENERIC
+    cfg = tile_config(_Fake((64, 64), (64, 1), ptr=4098), _Fake((64, 64), (64, 1)))
     assert cfg["family"] == "generic"
 
 

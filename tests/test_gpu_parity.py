@@ -76,8 +76,9 @@ def test_fp32_accumulate_mode():
 
 
 def test_strided_operands_use_generic_path():
-    a_big, b_big = rnd((300, 512), 6), rnd((256, 700), 7)
-    a, b = a_big[:, ::2], b_big[:, 1::3]  # strides (512, 2) and (700, 3)
+    # 300 x 233 x 200: below the size where mm packs strided operands
+    a_big, b_big = rnd((300, 400), 6), rnd((200, 700), 7)
+    a, b = a_big[:, ::2], b_big[:, 1::3]  # strides (400, 2) and (700, 3)
     ga, gb = a_big.cuda()[:, ::2], b_big.cuda()[:, 1::3]
     cfg = tile_config(ga, gb)
     assert cfg["family"] == "generic"
@@ -122,7 +123,7 @@ def test_zero_sizes():
     assert c.shape == (64, 0)
 
 
-@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic"])
+@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic", "64x64"])
 @pytest.mark.parametrize("K", [64, 128, 192, 200, 320, 1024])
 def test_every_tile_matches_oracle(tile, K):
     """Each tile configuration, forced, on ragged M/N edges, for K of one to
@@ -146,7 +147,7 @@ def test_every_tile_matches_oracle(tile, K):
         assert rel(c32.cpu(), (a.float() @ b.float()).double()) < 1e-5
 
 
-@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic"])
+@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic", "64x64"])
 def test_every_tile_redoes_overflowing_tiles(tile):
     """Overflow closed form (reference tests/test_f16acc.py:91-101) placed in
     one tile of a larger grid: that tile is flagged and exact, the others not."""
@@ -246,7 +247,10 @@ def test_overflow_stress_flags_exactly_the_block_intersections():
     ref, rflags = oracle(a, b, torch.float32, cfg)
     assert torch.equal(flags.cpu(), rflags)
     bm, bn = cfg["bm"], cfg["bn"]
-    want = {(r * 128 // bm, q * 128 // bn) for r in rows for q in cols}
+    # each overflowing block is 128 x 128: it covers one tile of 128 or more,
+    # or 128 / bm x 128 / bn smaller tiles
+    sm, sn = max(1, 128 // bm), max(1, 128 // bn)
+    want = {(r * 128 // bm + i, q * 128 // bn + j) for r in rows for q in cols for i in range(sm) for j in range(sn)}
     assert {tuple(t) for t in flags.nonzero().tolist()} == want
     mask = flags.bool().repeat_interleave(bm, 0).repeat_interleave(bn, 1)[:1024, :1024]
     assert torch.equal(c[mask], c32[mask])
