@@ -31,6 +31,7 @@ typedef _Float16 f16;
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x8 __attribute__((ext_vector_type(8)));
 
 #define CHECK(x)                                                                   \
   do {                                                                             \
@@ -101,10 +102,32 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 #define MIX_LO(s, h) asm volatile("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel_hi:[1,0,0]" : "+v"(s) : "v"(h))
 #define MIX_HI(s, h) asm volatile("v_fma_mix_f32 %0, %1, 1.0, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(s) : "v"(h))
 #define DOT2(s, h) asm volatile("v_dot2c_f32_f16 %0, %1, %2" : "+v"(s) : "v"(h), "v"(ones))
+#define SMFMAC(acc, a, b, idx) \
+  asm volatile("v_smfmac_f32_16x16x64_f16 %0, %1, %2, %3" : "+v"(acc) : "v"(a), "v"(b), "v"(idx))
+
+// Sparse selector of a chunk quad: with B = {X_odd, X_even} (the rounded
+// pairs of one 16x16 block from two consecutive stages, dense 16x16x32 B
+// layout each: elements 0-7 are K 0-31, elements 8-15 are K 32-63), A row i
+// is 1 at K = 2i, 2i+1, 32+2i, 33+2i: lane 16q+i holds K 16q..16q+15 as four
+// groups of 4 with two stored values each; rows i with q == i/8 or
+// q == 2 + i/8 store (1, 1) at positions 2(i%2), 2(i%2)+1 of group (i%8)/2.
+__device__ __forceinline__ void quad_selector(int lane, f16x8& a, int& idx) {
+  const int q = lane >> 4, i = lane & 15, g = (i & 7) >> 1, p = 2 * (i & 1);
+  const bool on = q == (i >> 3) || q == 2 + (i >> 3);
+  idx = 0;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) a[c] = (on && c / 2 == g) ? (f16)1.0f : (f16)0.0f;
+#pragma unroll
+  for (int gg = 0; gg < 4; ++gg) idx |= (gg == g ? (p | ((p + 1) << 2)) : (0 | (1 << 2))) << (4 * gg);
+}
 
 // E: 0 FP32-accumulating MFMAs (the reference's chunked=False), 1 cvt_pk + dot2,
 //    2 cvt_pk + fma_mix, 3 cvt_pk + selector MFMA (the shipped epilogue),
-//    4 cvt_pk alone (no sum: a lower bound)
+//    4 cvt_pk alone (no sum: a lower bound),
+//    5 cvt_pk + sparse selector (one v_smfmac_f32_16x16x64_f16 per block per
+//      two stages; the two stages' rounded pairs joined into one 8-register
+//      operand), 6 as 5 with the rounding written straight into that operand
+//    (5 and 6 run an even and an odd stage per iteration: 2 NB steps)
 template <int E>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void epilogue_kernel(
     float* out, int iters, unsigned long long* cyc) {
@@ -129,8 +152,54 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     p0[j] = p1[j] = S[j] = f32x4{0.f, 0.f, 0.f, (float)j};
     h[j] = u32x4{0u, 0u, 0u, 0u};
   }
+  f16x8 sel4;
+  int idx;
+  quad_selector(lane, sel4, idx);
+  u32x4 hs[NB];
+  u32x8 X[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    hs[j] = u32x4{0u, 0u, 0u, 0u};
+    X[j] = u32x8{0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+  }
   const unsigned long long t0 = __builtin_amdgcn_s_memtime();
   for (int it = 0; it < iters; ++it) {
+    if (E == 5 || E == 6) {
+#pragma unroll
+      for (int pass = 0; pass < 2; ++pass)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          const int q = (j + NB - 2) % NB;
+          MFMA_ZERO(p0[j], b[j], a0);
+          if (E == 5) {
+            u32x4& d = pass ? h[q] : hs[q];
+            CVT_PK(d[0], p0[q][0], p1[q][0]);
+            CVT_PK(d[1], p0[q][1], p1[q][1]);
+          } else {
+            CVT_PK(X[q][4 * pass + 0], p0[q][0], p1[q][0]);
+            CVT_PK(X[q][4 * pass + 1], p0[q][1], p1[q][1]);
+          }
+          MFMA_ZERO(p1[j], b[j], a1);
+          if (E == 5) {
+            u32x4& d = pass ? h[q] : hs[q];
+            CVT_PK(d[2], p0[q][2], p1[q][2]);
+            CVT_PK(d[3], p0[q][3], p1[q][3]);
+          } else {
+            CVT_PK(X[q][4 * pass + 2], p0[q][2], p1[q][2]);
+            CVT_PK(X[q][4 * pass + 3], p0[q][3], p1[q][3]);
+          }
+          if (pass == 1) {
+            const int r = (j + NB - 3) % NB;
+            if (E == 5) {
+              const u32x8 bb = __builtin_shufflevector(h[r], hs[r], 0, 1, 2, 3, 4, 5, 6, 7);
+              SMFMAC(S[r], sel4, bb, idx);
+            } else {
+              SMFMAC(S[r], sel4, X[r], idx);
+            }
+          }
+        }
+      continue;
+    }
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int q = (j + NB - 2) % NB;  // block whose epilogue runs now: its MFMAs are 4 MFMAs old
@@ -166,7 +235,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const unsigned long long t1 = __builtin_amdgcn_s_memtime();
   float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < NB; ++j) s += S[j][0] + S[j][3] + p0[j][1] + p1[j][2] + (float)h[j][1];
+  for (int j = 0; j < NB; ++j) s += S[j][0] + S[j][3] + p0[j][1] + p1[j][2] + (float)h[j][1] + (float)hs[j][2] + (float)X[j][5];
   out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
   if (threadIdx.x == 0) cyc[blockIdx.x] = t1 - t0;
 }
@@ -227,14 +296,17 @@ int main() {
     part1_row<7>(b, w);
     std::printf("part 2: chunk-pair epilogues; cycles per block step (2 chunk MFMAs = 32 ideal), fraction of peak\n");
     const char* names[] = {"FP32-accumulating MFMAs", "cvt_pk x4 + dot2 x4", "cvt_pk x4 + fma_mix x8",
-                           "cvt_pk x4 + selector MFMA", "cvt_pk x4 alone (bound)"};
-    double c[5];
+                           "cvt_pk x4 + selector MFMA", "cvt_pk x4 alone (bound)",
+                           "cvt_pk x4 + 1/2 smfmac (copy)", "cvt_pk x4 + 1/2 smfmac (in place)"};
+    double c[7];
     c[0] = measure(epilogue_kernel<0>, b, 8, w);
     c[1] = measure(epilogue_kernel<1>, b, 8, w);
     c[2] = measure(epilogue_kernel<2>, b, 8, w);
     c[3] = measure(epilogue_kernel<3>, b, 8, w);
     c[4] = measure(epilogue_kernel<4>, b, 8, w);
-    for (int i = 0; i < 5; ++i) std::printf("  %-28s %8.2f  %.3f\n", names[i], c[i], 32.0 / c[i]);
+    c[5] = measure(epilogue_kernel<5>, b, 16, w);
+    c[6] = measure(epilogue_kernel<6>, b, 16, w);
+    for (int i = 0; i < 7; ++i) std::printf("  %-33s %8.2f  %.3f\n", names[i], c[i], 32.0 / c[i]);
     CHECK(hipFree(b.out));
     CHECK(hipFree(b.cyc));
   }
