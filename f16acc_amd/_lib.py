@@ -50,6 +50,10 @@ block_tile = _dll.f16acc_block_tile
 block_tile.argtypes = [_i64, _i64, _i64, _P64, _P64]
 block_tile.restype = _int
 
+tail_split = _dll.f16acc_tail_split
+tail_split.argtypes = [_i64] * 7 + [_vp, _vp, _P64]
+tail_split.restype = _int
+
 strerror = _dll.f16acc_strerror
 strerror.argtypes = [_int]
 strerror.restype = ctypes.c_char_p
@@ -60,7 +64,7 @@ abi_version.restype = _int
 
 # Exported symbol names, as declared in include/f16acc.h.
 EXPORTS = ("f16acc_gemm", "f16acc_gemm_bias", "f16acc_gemm_ws", "f16acc_workspace_size", "f16acc_gemm_tile", "f16acc_pack", "f16acc_tile_config", "f16acc_block_tile", "f16acc_strerror",
-           "f16acc_abi_version")
+           "f16acc_abi_version", "f16acc_tail_split")
 ABI_VERSION = 2
 
 OUT_F16, OUT_F32 = 0, 1

@@ -901,7 +901,9 @@ constexpr double kTileRate[4] = {1.00, 0.87, 0.87, 0.89};
 constexpr double kSmallTileRate = 0.65;
 constexpr int kMinSplitStages = 16;
 
-inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus) {
+// est (optional) receives the estimated time of the pick, in the units of the
+// estimate that decided it.
+inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = nullptr) {
   int best = 0;
   double best_t = 0;
   for (int id = 0; id < 4; ++id) {
@@ -921,9 +923,45 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus) {
     const double est_best = (double)t.bm * t.bn * t.per_cu / kTileRate[best];
     const double est_small =
         (double)cdiv(stiles, (int64_t)cus * s.per_cu) * s.bm * s.bn * s.per_cu / kSmallTileRate;
-    if (est_small < est_best * 0.999) return F16ACC_TILE_64x64;
+    if (est_small < est_best * 0.999) {
+      if (est) *est = est_small;
+      return F16ACC_TILE_64x64;
+    }
+    if (est) *est = est_best;
+    return best;
   }
+  if (est) *est = best_t;
   return best;
+}
+
+// Ragged last round on the 256x256 tile.  When a shape's 256x256 tiles fill
+// some whole rounds of the CUs plus a few more (Qwen2.5-1.5B gate/up,
+// 2048x8960: 280 tiles on 256 CUs), the table would otherwise fall back to a
+// smaller tile everywhere, or run a second 256x256 round on a tenth of the
+// GPU.  Instead the problem is cut at a tile-column boundary: the first
+// nsplit columns as whole rounds of 256x256 tiles, the remaining columns as a
+// second GEMM with the table's own choice for that narrower shape (64x64
+// there: four times the tiles of 128x128 fill the GPU).  Both are ordinary
+// whole-K launches on the same stream, so every output element is computed
+// exactly as in a single launch; only the tile each element's overflow redo
+// covers differs, which the reference leaves to its autotuner as well.
+// Taken when the estimate (the table's units) gains at least 3 %.
+inline bool plan_tail(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                      const void* a, const void* b, int cus, int64_t* nsplit) {
+  const TileInfo& t = kTiles[F16ACC_TILE_256x256];
+  if (fast_layout(N, K, sam, sak, sbk, sbn, a, b, t.bm, t.bn) < 0) return false;
+  const int64_t tm = cdiv(M, t.bm), tn = cdiv(N, t.bn), tiles = tm * tn;
+  const int64_t rounds = tiles / cus;
+  if (rounds < 1 || tiles % cus == 0) return false;
+  const int64_t nmain = rounds * cus / tm;  // tile columns of the main part
+  if (nmain < 1 || nmain >= tn) return false;
+  double whole = 0, tail = 0;
+  choose_tile(M, N, K, cus, &whole);
+  choose_tile(M, N - nmain * t.bn, K, cus, &tail);
+  const double mixed = (double)cdiv(tm * nmain, cus) * t.bm * t.bn / kTileRate[F16ACC_TILE_256x256] + tail;
+  if (!(mixed < 0.97 * whole)) return false;
+  *nsplit = nmain * t.bn;  // 256-column steps keep the tail's operands 16-byte aligned
+  return true;
 }
 
 struct Choice {
@@ -1023,6 +1061,18 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
   if (forced_tile < -1 || forced_tile >= F16ACC_NUM_TILES) return F16ACC_E_ARG;
   if (M == 0 || N == 0) return 0;  // nothing to write (Triton skips an empty grid too)
   if (!c || (K > 0 && (!a || !b))) return F16ACC_E_ARG;
+  // A caller asking for tile flags gets one grid, the one f16acc_tile_config
+  // describes; otherwise a ragged last 256x256 round may become a second launch.
+  int64_t nsplit = 0;
+  if (forced_tile < 0 && !tile_flags && K > 0 && plan_tail(M, N, K, sam, sak, sbk, sbn, a, b, cu_count(), &nsplit)) {
+    const int esize = out_dtype == F16ACC_OUT_F32 ? 4 : 2;
+    const int rc = gemm_impl(a, b, bias, c, nullptr, M, nsplit, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked,
+                             stream, F16ACC_TILE_256x256);
+    if (rc != 0) return rc;
+    return gemm_impl(a, (const f16*)b + nsplit * sbn, bias ? (const f16*)bias + nsplit : nullptr,
+                     (char*)c + nsplit * scn * esize, nullptr, M, N - nsplit, K, sam, sak, sbk, sbn, scm, scn,
+                     out_dtype, chunked, stream, -1, workspace, ws_bytes);
+  }
   const Choice ch = choose(M, N, K, sam, sak, sbk, sbn, a, b, forced_tile);
   Params p;
   p.a = (const f16*)a;
@@ -1090,6 +1140,17 @@ int f16acc_block_tile(int64_t block, int64_t tiles_m, int64_t tiles_n, int64_t* 
   if (tiles_m <= 0 || tiles_n <= 0 || block < 0 || block >= tiles_m * tiles_n || !tile_m || !tile_n)
     return F16ACC_E_ARG;
   block_tile(block, tiles_m, tiles_n, tile_m, tile_n);
+  return 0;
+}
+
+int f16acc_tail_split(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                      const void* a, const void* b, int64_t* nsplit) {
+  if (M < 0 || N < 0 || K < 0 || !nsplit) return F16ACC_E_ARG;
+  *nsplit = 0;
+  if (M > 0 && N > 0 && K > 0) {
+    int64_t at = 0;
+    if (plan_tail(M, N, K, sam, sak, sbk, sbn, a, b, cu_count(), &at)) *nsplit = at;
+  }
   return 0;
 }
 

@@ -172,6 +172,17 @@ int f16acc_pack(const void* src, void* dst, int64_t rows, int64_t cols,
 int f16acc_block_tile(int64_t block, int64_t tiles_m, int64_t tiles_n,
                       int64_t* tile_m, int64_t* tile_n);
 
+/*
+ * Launch plan check: *nsplit receives the output column at which
+ * f16acc_gemm (without tile flags) cuts a problem whose 256x256 tiles fill
+ * whole rounds of the CUs plus a small ragged round: columns [0, nsplit) run
+ * as 256x256 tiles, [nsplit, N) as a second launch with the table's choice
+ * for that shape.  0 when the problem runs as one grid.  No counterpart in
+ * the reference (one Triton grid per call); exposed for host-side checks.
+ */
+int f16acc_tail_split(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                      const void* a, const void* b, int64_t* nsplit);
+
 /* Short text for a return code of this library (never NULL). */
 const char* f16acc_strerror(int code);
 

@@ -184,3 +184,21 @@ def test_patch_enable_disable_and_cpu_fallback():
     assert patch.MIN_ROWS == 128
     assert f16acc.calls is patch.calls
     assert set(f16acc.__all__) == {"mm", "enable", "disable", "calls"}
+
+
+@pytest.mark.parametrize("M,N,K,want", [
+    (2048, 8960, 1536, 8192),   # Qwen2.5-1.5B gate/up: 280 tiles of 256x256 on 256 CUs
+    (8192, 8960, 1536, 8192),   # 1120 tiles: four rounds plus 96
+    (2048, 8960, 8960, 8192),   # long K: the tail may split along K instead
+    (4096, 4096, 4096, 0),      # whole rounds
+    (2048, 151936, 1536, 0),    # lm_head: the ragged round is half full, a tail gains < 3 %
+    (2048, 1536, 1536, 0),      # under one round
+])
+def test_ragged_round_tail_plan(M, N, K, want):
+    """Where f16acc_gemm cuts a ragged last 256x256 round into a second launch
+    (no GPU here: the planner assumes 256 CUs)."""
+    n = ctypes.c_int64(-1)
+    _lib.check(_lib.tail_split(M, N, K, K, 1, 1, K, 0, 0, ctypes.byref(n)))
+    assert n.value == want
+    assert _lib.tail_split(-1, N, K, K, 1, 1, K, 0, 0, ctypes.byref(n)) == -1  # F16ACC_E_ARG
+

@@ -365,3 +365,63 @@ def test_split_k_bias_and_ws_entry_without_workspace():
                      256, 1, 0, 1, st) == 0
     assert torch.equal(c, plain)
     assert rel(c.cpu(), chunk32.mm(x.cpu(), w.cpu().t(), torch.float16, tile=(128, 128))) < TOL
+
+
+def _tail_split(ga, gb):
+    import ctypes
+
+    from f16acc_amd import _lib
+
+    n = ctypes.c_int64()
+    M, K = ga.shape
+    _lib.check(_lib.tail_split(M, gb.shape[1], K, ga.stride(0), ga.stride(1), gb.stride(0), gb.stride(1),
+                               ga.data_ptr(), gb.data_ptr(), ctypes.byref(n)))
+    return n.value
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+def test_ragged_round_tail_split_equals_single_grid(out_dtype):
+    """Qwen2.5-1.5B gate/up (2048 x 8960 x 1536, w.t()): 280 tiles of 256x256
+    for 256 CUs.  mm runs columns 0..8191 as one round of 256x256 tiles and
+    the last 768 as a second launch; every element is computed as in the
+    single grid mm_flags launches (bit for bit) and matches the oracle."""
+    x, w = rnd((2048, 1536), 80), rnd((8960, 1536), 81, 0.05)
+    gx, gw = x.cuda(), w.cuda()
+    assert _tail_split(gx, gw.t()) == 8192
+    c = f16acc.mm(gx, gw.t(), out_dtype)
+    c1, flags = mm_flags(gx, gw.t(), out_dtype)
+    assert int(flags.sum()) == 0
+    assert torch.equal(c, c1)
+    assert rel(c.cpu(), chunk32.mm(x, w.t(), out_dtype, tile=(128, 128))) < TOL
+
+
+def test_ragged_round_tail_split_redoes_overflow_in_both_launches():
+    """The reference's forced-overflow closed form (tests/test_f16acc.py:91-101:
+    chunk sums of +-96000, exact result 100) in output columns 500..509 (the
+    256x256 launch) and 8500..8509 (the tail launch): both come out exact."""
+    x, w = rnd((2048, 1536), 82, 0.5), rnd((8960, 1536), 83, 0.5)
+    x[100:110, :] = 100.0
+    for c0 in (500, 8500):
+        cols = slice(c0, c0 + 10)
+        w[cols, :] = 0.0
+        w[cols, 0:32], w[cols, 32:64], w[cols, 64:96], w[cols, 96:128] = 30.0, -30.0, 30.0, -30.0
+        w[cols, 127] = -29.0
+    gx, gw = x.cuda(), w.cuda()
+    assert _tail_split(gx, gw.t()) == 8192
+    c = f16acc.mm(gx, gw.t(), torch.float32)
+    assert torch.all(c[100:110, 500:510] == 100.0) and torch.all(c[100:110, 8500:8510] == 100.0)
+    assert rel(c.cpu(), chunk32.mm(x, w.t(), torch.float32, tile=(128, 128))) < TOL
+
+
+def test_ragged_round_tail_split_fused_bias():
+    """The tail launch gets the bias from its first column on: the fused
+    result still equals the unfused y = mm(x2, w.t()); y += b bit for bit."""
+    from f16acc_amd import patch
+
+    x, w, bias = rnd((2048, 1536), 84).cuda(), rnd((8960, 1536), 85, 0.02).cuda(), rnd((8960,), 86, 0.5).cuda()
+    assert _tail_split(x, w.t()) == 8192
+    unfused = f16acc.mm(x, w.t())
+    unfused += bias
+    with torch.no_grad():
+        assert torch.equal(patch.linear(x, w, bias), unfused)
+
