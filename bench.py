@@ -17,7 +17,8 @@ redo.  Prints one JSON line:
   cpu_baseline the reference algorithm (the CPU oracle) on this host's cores
   hipblaslt   torch.mm (hipBLASLt) on the same inputs and GPU
   max_rel_err_vs_fp64 / max_rel_err_vs_oracle  the reference's error metric
-Other workloads (--workload) are sweeps for the design record, not bench lines.
+Other workloads (--workload) are sweeps for the design record, not bench lines;
+--workload shapes reports every configured shape against hipBLASLt.
 """
 
 import argparse
@@ -41,11 +42,13 @@ TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_4096_fp16out_rowmajorB_tr
 
 WORKLOADS = {
     # name: (M, N, K, b_layout, out_dtype)
+    "gemm1024_f32": (1024, 1024, 1024, "row", torch.float32),
     "gemm4096": (4096, 4096, 4096, "row", torch.float16),
     "gemm4096_bt": (4096, 4096, 4096, "t", torch.float16),
     "gemm4096_f32": (4096, 4096, 4096, "row", torch.float32),
     "gemm8192": (8192, 8192, 8192, "row", torch.float16),
     "gemm8192_bt": (8192, 8192, 8192, "t", torch.float16),
+    "gemm8192_f32": (8192, 8192, 8192, "row", torch.float32),
     "qwen_qo": (2048, 1536, 1536, "t", torch.float16),
     "qwen_kv": (2048, 256, 1536, "t", torch.float16),
     "qwen_gateup": (2048, 8960, 1536, "t", torch.float16),
@@ -163,6 +166,85 @@ def sweep_tiles(names, rounds=5):
         print(json.dumps(row), flush=True)
         del a, b
         torch.cuda.empty_cache()
+
+
+def settled_time(op, burst_ms=40.0):
+    """Seconds per call in the second half of a ~burst_ms back-to-back burst
+    (HIP events): the first half lets the clock settle after the previous op."""
+    op()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    op()
+    e.record()
+    torch.cuda.synchronize()
+    n = max(10, int(burst_ms / max(s.elapsed_time(e), 0.01)))
+    for _ in range(n // 2):
+        op()
+    s.record()
+    for _ in range(n - n // 2):
+        op()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / 1e3 / (n - n // 2)
+
+
+def shapes_report(names, rounds=4):
+    """TFLOPS at every configured shape, as absolute numbers and as a fraction
+    of the MI355X dense fp16 MFMA peak: mm as shipped (chunked, the per-shape
+    table, packing and split-K included), its FP32-accumulate mode, and
+    hipBLASLt (torch.mm, fp16 out) on the same inputs, timed in interleaved
+    ~40 ms bursts (median over rounds of each burst's settled second half),
+    plus mm's max relative error against an FP64 GEMM of the same inputs."""
+    import f16acc_amd
+    from f16acc_amd.kernel import tile_config
+
+    torch.backends.cuda.matmul.allow_fp16_reduced_precision_reduction = False
+    rows = []
+    for name in names:
+        M, N, K, layout, out_dtype = WORKLOADS[name]
+        _, _, a, b = make_inputs(M, N, K, layout)
+        flops = 2.0 * M * N * K
+        ops = {"mm": lambda: f16acc_amd.mm(a, b, out_dtype),
+               "fp32acc": lambda: f16acc_amd.mm(a, b, out_dtype, chunked=False),
+               "hipblaslt": lambda: torch.mm(a, b)}
+        times = {k: [] for k in ops}
+        for _ in range(rounds):
+            for k, op in ops.items():
+                times[k].append(settled_time(op))
+        c = f16acc_amd.mm(a, b, out_dtype)
+        ref = a.double() @ b.double()
+        err = ((c.double() - ref).abs().max() / ref.abs().max()).item()
+        del c, ref
+        import ctypes
+
+        from f16acc_amd import _lib
+
+        nsplit = ctypes.c_int64()
+        _lib.check(_lib.tail_split(M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1), a.data_ptr(),
+                                   b.data_ptr(), ctypes.byref(nsplit)))
+        table = tile_config(a, b)["tile"]
+        if nsplit.value:
+            table = f"256x256 for n < {nsplit.value}, then {tile_config(a[:, :], b[:, nsplit.value:])['tile']}"
+        row = {"workload": name, "M": M, "N": N, "K": K, "b": "row-major [K,N]" if layout == "row" else "w.t()",
+               "out": "fp16" if out_dtype == torch.float16 else "fp32", "table": table,
+               "max_rel_err_vs_fp64": float(f"{err:.3g}")}
+        for k, v in times.items():
+            t = statistics.median(v)
+            row[k] = {"us": round(t * 1e6, 1), "tflops": round(flops / t / 1e12, 1),
+                      "frac_of_peak": round(flops / t / 1e12 / PEAK_TFLOPS, 3)}
+        row["mm_vs_hipblaslt"] = round(row["hipblaslt"]["us"] / row["mm"]["us"], 3)
+        print(json.dumps(row), flush=True)
+        rows.append(row)
+        del a, b
+        torch.cuda.empty_cache()
+    print("\n| shape | out | B | table tile | mm us | mm TFLOPS | frac of peak | FP32-acc TFLOPS | hipBLASLt TFLOPS |"
+          " mm / hipBLASLt | max rel err vs FP64 |")
+    print("|---|---|---|---|---|---|---|---|---|---|---|")
+    for r in rows:
+        print(f"| {r['M']}x{r['N']}x{r['K']} | {r['out']} | {r['b']} | {r['table']} | {r['mm']['us']} | "
+              f"{r['mm']['tflops']} | {r['mm']['frac_of_peak']} | {r['fp32acc']['tflops']} | "
+              f"{r['hipblaslt']['tflops']} | {r['mm_vs_hipblaslt']} | {r['max_rel_err_vs_fp64']:.2e} |")
 
 
 def burst_time(op, warmup=3, calls=5):
@@ -331,7 +413,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="gemm4096", choices=sorted(WORKLOADS) + ["copy", "overflow", "qwen2_prefill"])
+    ap.add_argument("--workload", default="gemm4096",
+                    choices=sorted(WORKLOADS) + ["copy", "overflow", "qwen2_prefill", "shapes"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and oracle comparison")
     ap.add_argument("--preheat", type=float, default=PREHEAT_S,
                     help="seconds of back-to-back calls before the warm-up steps (0 for counter runs)")
@@ -347,6 +430,8 @@ def main():
 
     if args.workload == "copy":
         return copy_reference(args.steps, args.warmup)
+    if args.workload == "shapes":
+        return shapes_report(list(WORKLOADS))
     if args.workload == "overflow":
         return overflow_bench(args.steps, args.warmup)
     if args.workload == "qwen2_prefill":
