@@ -889,17 +889,33 @@ constexpr double kTileRate[4] = {1.00, 0.87, 0.87, 0.89};
 // The per-shape table: the fast tile with the smallest estimated time.
 // Ties keep the larger tile.
 //
-// Small grids: when the pick leaves workgroup slots empty and K is too short
-// for a split (fewer than 2 x kMinSplitStages stages), the 64x64 tile is
+// Small grids: when the pick leaves workgroup slots empty, the 64x64 tile is
 // weighed against it by rounds of full-occupancy workgroups:
 //   estimated time = ceil(tiles / (CUs x per_cu)) x tile area x per_cu / rate
-// (64x64 runs three workgroups per CU, each wave 32x32: it reads twice the
-// LDS per MFMA of a 64x64 wave tile, rate 0.65, but four times the tiles
-// fill the GPU: Qwen2.5-1.5B k/v 2048x256x1536 20.0 -> 11.3 us, q/o
-// 2048x1536x1536 21.6 -> 19.7 us; gate/up 2048x8960x1536 stays on 128x128,
-// 83.6 us against 101 us).
+// where the pick may also split K (plan_split; the split's own estimate
+// divides by the split count and adds kSplitCost for the second launch and
+// the partials' traffic).  64x64 runs three workgroups per CU, each wave
+// 32x32: it reads twice the LDS per MFMA of a 64x64 wave tile (rate 0.65),
+// but four times the tiles fill the GPU.  Measured: Qwen2.5-1.5B k/v
+// 2048x256x1536 20.0 -> 11.3 us and q/o 2048x1536x1536 21.6 -> 19.7 us
+// against 128x128; down 2048x1536x8960 92-96 us, as fast as 128x128 split
+// in two and in one launch; gate/up 2048x8960x1536 stays off 64x64 (101 us
+// against 83.6 us on 128x128).
 constexpr double kSmallTileRate = 0.65;
+constexpr double kSplitCost = 1.08;
 constexpr int kMinSplitStages = 16;
+constexpr int kMaxSplits = 16;
+
+// The split count plan_split uses for a tile with `tiles` tiles, `slots`
+// workgroup slots and nsteps LDS stages: as many splits as fill the slots,
+// each split keeping at least kMinSplitStages stages, at most kMaxSplits.
+inline int64_t split_count(int64_t tiles, int64_t slots, int64_t nsteps) {
+  int64_t want = slots / tiles;
+  if (want > kMaxSplits) want = kMaxSplits;
+  if (want > nsteps / kMinSplitStages) want = nsteps / kMinSplitStages;
+  if (want < 2) return 1;
+  return cdiv(nsteps, cdiv(nsteps, want));  // whole splits of equal stage counts
+}
 
 // est (optional) receives the estimated time of the pick, in the units of the
 // estimate that decided it.
@@ -917,10 +933,15 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
   }
   const TileInfo& t = kTiles[best];
   const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn), slots = (int64_t)cus * t.per_cu;
-  if (tiles < slots && cdiv(K, kStageK) < 2 * kMinSplitStages) {
+  if (tiles < slots) {
     const TileInfo& s = kTiles[F16ACC_TILE_64x64];
     const int64_t stiles = cdiv(M, s.bm) * cdiv(N, s.bn);
-    const double est_best = (double)t.bm * t.bn * t.per_cu / kTileRate[best];
+    double est_best = (double)t.bm * t.bn * t.per_cu / kTileRate[best];
+    const int64_t splits = best == F16ACC_TILE_256x256 ? 1 : split_count(tiles, slots, cdiv(K, kStageK));
+    if (splits > 1) {
+      const double est_split = (double)cdiv(tiles * splits, slots) * est_best / splits * kSplitCost;
+      if (est_split < est_best) est_best = est_split;
+    }
     const double est_small =
         (double)cdiv(stiles, (int64_t)cus * s.per_cu) * s.bm * s.bn * s.per_cu / kSmallTileRate;
     if (est_small < est_best * 0.999) {
@@ -1023,7 +1044,6 @@ hipError_t launch_finish(const Params& p, int out32, int chunked, hipStream_t st
 // launch and the partials' traffic only pay off on long K (measured: the
 // Qwen2.5 down projection, K = 8960, gains; K = 1536 loses), so each split
 // keeps at least kMinSplitStages LDS stages; at most kMaxSplits.
-constexpr int kMaxSplits = 16;
 
 struct SplitPlan {
   int splits;
@@ -1033,19 +1053,15 @@ struct SplitPlan {
 
 inline SplitPlan plan_split(const Choice& ch, int64_t M, int64_t N, int64_t K, int cus) {
   SplitPlan sp{1, K, 0};
-  // 256x256 is not SPLITTABLE; 64x64 is only chosen where K is too short to split
+  // 256x256 is not SPLITTABLE; 64x64 fills the GPU with its own tiles (choose_tile)
   if (ch.family != F16ACC_FAMILY_FAST || ch.tile == F16ACC_TILE_256x256 || ch.tile == F16ACC_TILE_64x64) return sp;
   const TileInfo& t = kTiles[ch.tile];
   const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
   const int64_t slots = (int64_t)cus * t.per_cu;
   const int64_t nsteps = cdiv(K, kStageK);
-  int64_t want = slots / tiles;
-  if (want > kMaxSplits) want = kMaxSplits;
-  if (want > nsteps / kMinSplitStages) want = nsteps / kMinSplitStages;
-  if (want < 2) return sp;
-  const int64_t steps_per = cdiv(nsteps, want);
-  const int64_t splits = cdiv(nsteps, steps_per);
+  const int64_t splits = split_count(tiles, slots, nsteps);
   if (splits < 2) return sp;
+  const int64_t steps_per = cdiv(nsteps, splits);
   sp.splits = (int)splits;
   sp.kps = steps_per * kStageK;
   sp.bytes = (size_t)tiles * splits * t.bm * t.bn * sizeof(float);

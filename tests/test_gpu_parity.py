@@ -297,7 +297,7 @@ def _split_plan(ga, gb):
     return n.value
 
 
-@pytest.mark.parametrize("shape", [(256, 256, 4096), (2048, 256, 4096), (300, 200, 2100), (512, 384, 8960)])
+@pytest.mark.parametrize("shape", [(256, 256, 4096), (2048, 256, 4096), (300, 200, 4200), (512, 384, 8960)])
 def test_split_k_matches_oracle(shape):
     """Shapes with few output tiles are split along K into chunk-aligned
     ranges; a second launch adds the FP32 partials per tile.  Results and
@@ -315,7 +315,9 @@ def test_split_k_matches_oracle(shape):
         assert torch.equal(flags.cpu(), rflags)
         assert rel(c.cpu(), ref) < TOL, (shape, out_dtype)
         # the workspace is reused across calls: another split problem in between
-        f16acc.mm(rnd((64, 512), 1).cuda(), rnd((512, 64), 2).cuda())
+        other_a, other_b = rnd((256, 4096), 1).cuda(), rnd((4096, 256), 2).cuda()
+        assert _split_plan(other_a, other_b) > 0
+        f16acc.mm(other_a, other_b)
         again = f16acc.mm(ga, gb, out_dtype)
         assert torch.equal(again, c)
 
