@@ -448,6 +448,13 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
   constexpr bool kSpread = T >= 32;
   constexpr int kDmaEvery = T / (2 * kUnits) > 0 ? T / (2 * kUnits) : 1;
   if (!kSpread && has_next) next.all();
+  // Tiles of 4-wave workgroups run two or three workgroups per CU, so a
+  // SIMD's waves belong to workgroups in different phases: raising the
+  // priority of a wave in its MFMA loop over one in its barrier and copy
+  // phase measured +1.3-4.9 % on 128x128 (none on the 8-wave tiles, whose
+  // waves on a SIMD move in step).
+  constexpr bool kPrio = C::T <= 256;
+  if (kPrio) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const int i = t % C::FM, j = t / C::FM;
@@ -476,6 +483,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
       bcur[1] = bnext[1];
     }
   }
+  if (kPrio) __builtin_amdgcn_s_setprio(0);
 }
 
 // Whole K loop of the fast path: an NS-stage LDS ring.  The copies of the

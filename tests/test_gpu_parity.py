@@ -382,16 +382,20 @@ def _tail_split(ga, gb):
 
 
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
-def test_ragged_round_tail_split_equals_single_grid(out_dtype):
-    """Qwen2.5-1.5B gate/up (2048 x 8960 x 1536, w.t()): 280 tiles of 256x256
-    for 256 CUs.  mm runs columns 0..8191 as one round of 256x256 tiles and
-    the last 768 as a second launch; every element is computed as in the
-    single grid mm_flags launches (bit for bit) and matches the oracle."""
+@pytest.mark.parametrize("b_layout", ["w.t()", "row-major"])
+def test_ragged_round_tail_split_equals_single_grid(out_dtype, b_layout):
+    """Qwen2.5-1.5B gate/up (2048 x 8960 x 1536): 280 tiles of 256x256 for
+    256 CUs.  mm runs columns 0..8191 as one round of 256x256 tiles and the
+    last 768 as a second launch (B offset by 8192 columns: a row offset of
+    w, a column offset of a row-major [K, N]); every element is computed as
+    in the single grid mm_flags launches (bit for bit) and matches the
+    oracle."""
     x, w = rnd((2048, 1536), 80), rnd((8960, 1536), 81, 0.05)
-    gx, gw = x.cuda(), w.cuda()
-    assert _tail_split(gx, gw.t()) == 8192
-    c = f16acc.mm(gx, gw.t(), out_dtype)
-    c1, flags = mm_flags(gx, gw.t(), out_dtype)
+    gx = x.cuda()
+    gb = w.cuda().t() if b_layout == "w.t()" else w.t().contiguous().cuda()
+    assert _tail_split(gx, gb) == 8192
+    c = f16acc.mm(gx, gb, out_dtype)
+    c1, flags = mm_flags(gx, gb, out_dtype)
     assert int(flags.sum()) == 0
     assert torch.equal(c, c1)
     assert rel(c.cpu(), chunk32.mm(x, w.t(), out_dtype, tile=(128, 128))) < TOL
