@@ -19,14 +19,16 @@
 // so a chunk pair costs three MFMAs and four VALU conversions.  Measured on
 // MI355X, VALU work and MFMAs overlap only partly and v_dot2_f32_f16 stalls
 // the matrix pipe outright, so summing on the MFMA pipe is the faster form:
-// 3 MFMAs + 4 v_cvt_pk per block step run at ~0.63 of the plain FP32-
-// accumulating MFMA rate (ceiling 2/3), against ~0.46 for cvt + v_dot2.
-// The steps are software pipelined (see compute_stage) so no instruction
-// waits on the MFMA that produces its operand.
+// 3 MFMAs + 4 v_cvt_pk per block step run at ~0.65 of the plain FP32-
+// accumulating MFMA rate (ceiling 2/3), against ~0.47 for cvt + v_dot2.
+// The steps are software pipelined four deep, across stage boundaries (see
+// compute_stage), so no instruction waits on the MFMA that produces its
+// operand.
 //
 // Data path per workgroup: operand tiles are staged global -> LDS with
 // buffer_load_dwordx4 ... lds (no VGPR round trip), 64 K (two chunks) per
-// stage, two stages in flight.  Out-of-range 16-byte units (M/N/K edges) are
+// stage, in a ring of NS stages whose next NS-1 are in flight while one is
+// multiplied.  Out-of-range 16-byte units (M/N/K edges) are
 // zero-filled by the buffer range check, like the reference's masked loads
 // (kernel.py:45-47).  LDS layouts:
 //   KC  (operand K-contiguous: a row-major, or b given as w.t()):
