@@ -431,3 +431,75 @@ def test_ragged_round_tail_split_fused_bias():
     with torch.no_grad():
         assert torch.equal(patch.linear(x, w, bias), unfused)
 
+
+
+def test_concurrent_calls_on_two_streams_from_two_threads():
+    """mm keeps no shared state (the reference hands best_config to its redo
+    launch through a global, README.md:48): two host threads calling it on
+    their own streams, split-K and two-launch shapes included, get the same
+    bits as one thread alone."""
+    import threading
+
+    shapes = [(2048, 256, 4096), (2048, 8960, 1536), (300, 520, 640)]
+    inputs = [(rnd((M, K), 90 + i).cuda(), rnd((N, K), 95 + i, 0.05).cuda().t()) for i, (M, N, K) in enumerate(shapes)]
+    want = [f16acc.mm(a, b) for a, b in inputs]
+    torch.cuda.synchronize()
+    got = [[None] * len(inputs) for _ in range(2)]
+    errors = []
+
+    def worker(k):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for rep in range(3):
+                    for i, (a, b) in enumerate(inputs):
+                        got[k][i] = f16acc.mm(a, b)
+            s.synchronize()
+        except Exception as e:  # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(k,)) for k in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for k in range(2):
+        for i in range(len(inputs)):
+            assert torch.equal(got[k][i], want[i]), (k, shapes[i])
+
+
+def test_hip_graph_capture_replays_match_eager():
+    """mm captured in a HIP graph (one split-K shape, one two-launch shape,
+    one plain and one bias-fused call) and replayed three times, with eager
+    work on the same inputs between replays: every replay equals the eager
+    result bit for bit.  The library records no memset nodes; its workspace
+    and outputs come from the graph's pool."""
+    from f16acc_amd import patch
+
+    x1, w1 = rnd((2048, 4096), 100).cuda(), rnd((256, 4096), 101, 0.02).cuda()
+    x2, w2 = rnd((2048, 1536), 102).cuda(), rnd((8960, 1536), 103, 0.02).cuda()
+    x3, w3, b3 = rnd((512, 640), 104).cuda(), rnd((384, 640), 105, 0.05).cuda(), rnd((384,), 106, 0.5).cuda()
+
+    def run():
+        with torch.no_grad():
+            return f16acc.mm(x1, w1.t()), f16acc.mm(x2, w2.t()), patch.linear(x3, w3, b3), f16acc.mm(x3, w3.t())
+
+    eager = run()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()  # warm-up on the capture stream: its workspace exists before capture
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = run()
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e)
+        again = run()  # eager work between replays
+        torch.cuda.synchronize()
+        for o, e in zip(again, eager):
+            assert torch.equal(o, e)
