@@ -26,7 +26,7 @@ ARCH = "gfx950"
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-Wall", "-Wno-unused-function",
+    "-Wall", "-Wextra",
 ]
 HIP_FLAGS = COMMON_FLAGS + ["-fPIC", "-shared"]
 

@@ -321,7 +321,9 @@ __device__ __forceinline__ f16x8 chunk_pair_selector(int lane) {
   return s;
 }
 
-// Half h of round_pair: elements 4h .. 4h+3 of x from lanes r = 2h, 2h+1.
+// Half h of the rounding of a chunk pair: the FP32 partials P0, P1 of a
+// block's two chunks, element r of each, become elements 2r, 2r+1 of x for
+// r = 2h, 2h+1 (the whole pair, h = 0 and 1, fills x).
 __device__ __forceinline__ void round_half(const f32x4& p0, const f32x4& p1, f16x8& x, int h) {
 #pragma unroll
   for (int r = 2 * h; r < 2 * h + 2; ++r) {
@@ -330,18 +332,6 @@ __device__ __forceinline__ void round_half(const f32x4& p0, const f32x4& p1, f16
     x[2 * r] = v[0];
     x[2 * r + 1] = v[1];
   }
-}
-
-__device__ __forceinline__ f16x8 round_pair(const f32x4& p0, const f32x4& p1) {
-  f16x8 x;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const f32x2 pr = {p0[r], p1[r]};
-    const f16x2 h = __builtin_convertvector(pr, f16x2);  // v_cvt_pk_f16_f32: RNE, inf past 65504
-    x[2 * r] = h[0];
-    x[2 * r + 1] = h[1];
-  }
-  return x;
 }
 
 // State of the chunk pipeline carried from one stage into the next, so the
@@ -496,8 +486,8 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
 // overwrite, then that copy is issued and stage s is multiplied.
 template <class C, bool CHUNKED>
 __device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t n0, int64_t kbeg, int64_t kend,
-                                            char LDS_AS* smem, FastLoader<C>& ld, int tid, int wave, int wm, int wn,
-                                            int lane, f32x4 (&acc)[C::FM][C::FN]) {
+                                            char LDS_AS* smem, FastLoader<C>& ld, int wave, int wm, int wn, int lane,
+                                            f32x4 (&acc)[C::FM][C::FN]) {
   const int64_t nsteps = (kend - kbeg + kStageK - 1) / kStageK;
   if (nsteps <= 0) return;
 #pragma unroll
@@ -690,7 +680,7 @@ __device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, 
 #pragma unroll
         for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
       if (FAST)
-        k_loop_fast<C, false>(p, m0, n0, 0, p.K, smem, ld, tid, wave, wm, wn, lane, acc);
+        k_loop_fast<C, false>(p, m0, n0, 0, p.K, smem, ld, wave, wm, wn, lane, acc);
       else
         k_loop_generic<C, false>(p, m0, n0, smem, tid, wm, wn, lane, acc);
     }
@@ -748,7 +738,7 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void 
   FastLoader<C> ld;
   if (FAST) {
     ld.init(p, m0, n0, tid);
-    k_loop_fast<C, CHUNKED>(p, m0, n0, kbeg, kend, smem, ld, tid, wave, wm, wn, lane, acc);
+    k_loop_fast<C, CHUNKED>(p, m0, n0, kbeg, kend, smem, ld, wave, wm, wn, lane, acc);
   } else {
     k_loop_generic<C, CHUNKED>(p, m0, n0, smem, tid, wm, wn, lane, acc);
   }
