@@ -503,3 +503,63 @@ def test_hip_graph_capture_replays_match_eager():
         torch.cuda.synchronize()
         for o, e in zip(again, eager):
             assert torch.equal(o, e)
+
+
+def _random_operand(g, rows, cols, kind, seed):
+    """A [rows, cols] fp16 CPU tensor laid out as `kind` (its GPU twin has the
+    same strides): contiguous, transposed view, strided view or offset view."""
+    n = 3 * max(rows, cols) + 5
+    base = rnd((n, n), seed)
+    if kind == "contiguous":
+        return base[:rows, :cols].contiguous()
+    if kind == "transposed":
+        return base[:cols, :rows].contiguous().t()
+    if kind == "strided":
+        return base[: 2 * rows : 2, : 3 * cols : 3]
+    return base[1 : rows + 1, 3 : cols + 3]  # offset view: misaligned rows
+
+
+@pytest.mark.parametrize("case", range(40))
+def test_randomized_shapes_layouts_and_tiles_match_oracle(case):
+    """Seeded random problems: M, N in 1..300, K in 0..700 (ragged chunks and
+    stages), each operand contiguous / transposed / strided / offset, fp16 or
+    fp32 output, chunked or not, the table's tile or a forced one; values and
+    tile flags against the oracle, some tiles overflowing on purpose."""
+    import random
+
+    from f16acc_amd import _lib
+
+    r = random.Random(1000 + case)
+    M, N, K = r.randint(1, 300), r.randint(1, 300), r.choice([0, 1, 7, 32, 33, 64, 96, 200, r.randint(1, 700)])
+    kinds = ["contiguous", "transposed", "strided", "offset"]
+    a = _random_operand(None, M, K, r.choice(kinds), 2000 + case)
+    b = _random_operand(None, K, N, r.choice(kinds), 3000 + case)
+    assert a.shape == (M, K) and b.shape == (K, N)
+    if K >= 64 and r.random() < 0.3:  # one overflowing block of rows x cols: chunk sums past 65504
+        i0, j0 = r.randrange(M), r.randrange(N)
+        a[i0 : i0 + 4, :] = 60.0
+        b[:, j0 : j0 + 4] = 60.0
+    out_dtype = r.choice([torch.float16, torch.float32])
+    chunked = r.random() < 0.8
+    tile = r.choice([None, None] + list(_lib.TILES))
+
+    def twin(t):
+        # same strides and offset on the GPU: copy the whole base storage
+        base = t.as_strided((t.untyped_storage().nbytes() // 2,), (1,), 0)
+        g = base.cuda()
+        return g.as_strided(t.shape, t.stride(), t.storage_offset())
+
+    ga, gb = twin(a), twin(b)
+    assert torch.equal(ga.cpu(), a) and torch.equal(gb.cpu(), b)
+    cfg = tile_config(ga, gb, tile)
+    c, flags = mm_flags(ga, gb, out_dtype, chunked, tile=tile)
+    ref, rflags = oracle(a, b, out_dtype, cfg, chunked=chunked)
+    assert c.shape == (M, N) and c.dtype == out_dtype
+    assert torch.equal(flags.cpu(), rflags), (case, M, N, K, tile)
+    finite = torch.isfinite(ref)
+    assert torch.equal(torch.isfinite(c.cpu()), finite), (case, M, N, K, tile)
+    if bool(finite.any()) and float(ref[finite].abs().max()) > 0:
+        err = (c.cpu()[finite].double() - ref[finite].double()).abs().max() / ref[finite].double().abs().max()
+        assert err < TOL, (case, M, N, K, tile, out_dtype, chunked, float(err))
+    else:
+        assert torch.equal(c.cpu()[finite], ref[finite])
