@@ -224,8 +224,10 @@ def shapes_report(names, rounds=4):
         _lib.check(_lib.tail_split(M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1), a.data_ptr(),
                                    b.data_ptr(), ctypes.byref(nsplit)))
         table = tile_config(a, b)["tile"]
-        if nsplit.value:
-            table = f"256x256 for n < {nsplit.value}, then {tile_config(a[:, :], b[:, nsplit.value:])['tile']}"
+        if nsplit.value > 0:
+            table = f"256x256 for n < {nsplit.value}, then {tile_config(a, b[:, nsplit.value:])['tile']}"
+        elif nsplit.value < 0:
+            table = f"256x256 for m < {-nsplit.value}, then {tile_config(a[-nsplit.value:], b)['tile']}"
         row = {"workload": name, "M": M, "N": N, "K": K, "b": "row-major [K,N]" if layout == "row" else "w.t()",
                "out": "fp16" if out_dtype == torch.float16 else "fp32", "table": table,
                "max_rel_err_vs_fp64": float(f"{err:.3g}")}

@@ -959,30 +959,51 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
 // some whole rounds of the CUs plus a few more (Qwen2.5-1.5B gate/up,
 // 2048x8960: 280 tiles on 256 CUs), the table would otherwise fall back to a
 // smaller tile everywhere, or run a second 256x256 round on a tenth of the
-// GPU.  Instead the problem is cut at a tile-column boundary: the first
-// nsplit columns as whole rounds of 256x256 tiles, the remaining columns as a
-// second GEMM with the table's own choice for that narrower shape (64x64
-// there: four times the tiles of 128x128 fill the GPU).  Both are ordinary
-// whole-K launches on the same stream, so every output element is computed
-// exactly as in a single launch; only the tile each element's overflow redo
-// covers differs, which the reference leaves to its autotuner as well.
-// Taken when the estimate (the table's units) gains at least 3 %.
+// GPU.  Instead the problem is cut at a tile boundary: the first `at`
+// columns (or rows, for tall problems) as whole rounds of 256x256 tiles, the
+// rest as a second GEMM with the table's own choice for that narrower shape
+// (64x64 there: four times the tiles of 128x128 fill the GPU).  Both are
+// ordinary whole-K launches on the same stream, so every output element is
+// computed exactly as in a single launch; only the tile each element's
+// overflow redo covers differs, which the reference leaves to its autotuner
+// as well.  Taken when the estimate (the table's units) gains at least 3 %;
+// on a tie the cut whose main part fills more of its rounds wins.
+struct TailPlan {
+  bool rows;   // cut along M (rows) instead of N (columns)
+  int64_t at;  // first row / column of the second launch, a multiple of 256
+};
+
 inline bool plan_tail(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
-                      const void* a, const void* b, int cus, int64_t* nsplit) {
+                      const void* a, const void* b, int cus, TailPlan* plan) {
   const TileInfo& t = kTiles[F16ACC_TILE_256x256];
   if (fast_layout(N, K, sam, sak, sbk, sbn, a, b, t.bm, t.bn) < 0) return false;
   const int64_t tm = cdiv(M, t.bm), tn = cdiv(N, t.bn), tiles = tm * tn;
   const int64_t rounds = tiles / cus;
   if (rounds < 1 || tiles % cus == 0) return false;
-  const int64_t nmain = rounds * cus / tm;  // tile columns of the main part
-  if (nmain < 1 || nmain >= tn) return false;
-  double whole = 0, tail = 0;
+  double whole = 0;
   choose_tile(M, N, K, cus, &whole);
-  choose_tile(M, N - nmain * t.bn, K, cus, &tail);
-  const double mixed = (double)cdiv(tm * nmain, cus) * t.bm * t.bn / kTileRate[F16ACC_TILE_256x256] + tail;
-  if (!(mixed < 0.97 * whole)) return false;
-  *nsplit = nmain * t.bn;  // 256-column steps keep the tail's operands 16-byte aligned
-  return true;
+  double best = 0.97 * whole;
+  int64_t best_fill = 0;
+  bool found = false;
+  for (int rows = 0; rows < 2; ++rows) {
+    const int64_t lines = rows ? tm : tn, across = rows ? tn : tm;
+    const int64_t main = rounds * cus / across;  // tile rows / columns of the main part
+    if (main < 1 || main >= lines) continue;
+    double tail = 0;
+    if (rows)
+      choose_tile(M - main * t.bm, N, K, cus, &tail);
+    else
+      choose_tile(M, N - main * t.bn, K, cus, &tail);
+    const double mixed = (double)cdiv(across * main, cus) * t.bm * t.bn / kTileRate[F16ACC_TILE_256x256] + tail;
+    if (mixed < best * 0.999 || (mixed <= best * 1.001 && across * main > best_fill)) {
+      best = mixed;
+      best_fill = across * main;
+      plan->rows = rows != 0;
+      plan->at = main * (rows ? t.bm : t.bn);  // 256-element steps keep the tail's operands 16-byte aligned
+      found = true;
+    }
+  }
+  return found;
 }
 
 struct Choice {
@@ -1079,15 +1100,23 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
   if (!c || (K > 0 && (!a || !b))) return F16ACC_E_ARG;
   // A caller asking for tile flags gets one grid, the one f16acc_tile_config
   // describes; otherwise a ragged last 256x256 round may become a second launch.
-  int64_t nsplit = 0;
-  if (forced_tile < 0 && !tile_flags && K > 0 && plan_tail(M, N, K, sam, sak, sbk, sbn, a, b, cu_count(), &nsplit)) {
+  TailPlan tp;
+  if (forced_tile < 0 && !tile_flags && K > 0 && plan_tail(M, N, K, sam, sak, sbk, sbn, a, b, cu_count(), &tp)) {
     const int esize = out_dtype == F16ACC_OUT_F32 ? 4 : 2;
-    const int rc = gemm_impl(a, b, bias, c, nullptr, M, nsplit, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked,
+    const int64_t at = tp.at;
+    if (tp.rows) {
+      const int rc = gemm_impl(a, b, bias, c, nullptr, at, N, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked,
+                               stream, F16ACC_TILE_256x256);
+      if (rc != 0) return rc;
+      return gemm_impl((const f16*)a + at * sam, b, bias, (char*)c + at * scm * esize, nullptr, M - at, N, K, sam,
+                       sak, sbk, sbn, scm, scn, out_dtype, chunked, stream, -1, workspace, ws_bytes);
+    }
+    const int rc = gemm_impl(a, b, bias, c, nullptr, M, at, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked,
                              stream, F16ACC_TILE_256x256);
     if (rc != 0) return rc;
-    return gemm_impl(a, (const f16*)b + nsplit * sbn, bias ? (const f16*)bias + nsplit : nullptr,
-                     (char*)c + nsplit * scn * esize, nullptr, M, N - nsplit, K, sam, sak, sbk, sbn, scm, scn,
-                     out_dtype, chunked, stream, -1, workspace, ws_bytes);
+    return gemm_impl(a, (const f16*)b + at * sbn, bias ? (const f16*)bias + at : nullptr,
+                     (char*)c + at * scn * esize, nullptr, M, N - at, K, sam, sak, sbk, sbn, scm, scn, out_dtype,
+                     chunked, stream, -1, workspace, ws_bytes);
   }
   const Choice ch = choose(M, N, K, sam, sak, sbk, sbn, a, b, forced_tile);
   Params p;
@@ -1164,8 +1193,8 @@ int f16acc_tail_split(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak,
   if (M < 0 || N < 0 || K < 0 || !nsplit) return F16ACC_E_ARG;
   *nsplit = 0;
   if (M > 0 && N > 0 && K > 0) {
-    int64_t at = 0;
-    if (plan_tail(M, N, K, sam, sak, sbk, sbn, a, b, cu_count(), &at)) *nsplit = at;
+    TailPlan tp;
+    if (plan_tail(M, N, K, sam, sak, sbk, sbn, a, b, cu_count(), &tp)) *nsplit = tp.rows ? -tp.at : tp.at;
   }
   return 0;
 }

@@ -173,12 +173,13 @@ int f16acc_block_tile(int64_t block, int64_t tiles_m, int64_t tiles_n,
                       int64_t* tile_m, int64_t* tile_n);
 
 /*
- * Launch plan check: *nsplit receives the output column at which
- * f16acc_gemm (without tile flags) cuts a problem whose 256x256 tiles fill
- * whole rounds of the CUs plus a small ragged round: columns [0, nsplit) run
- * as 256x256 tiles, [nsplit, N) as a second launch with the table's choice
- * for that shape.  0 when the problem runs as one grid.  No counterpart in
- * the reference (one Triton grid per call); exposed for host-side checks.
+ * Launch plan check: where f16acc_gemm (without tile flags) cuts a problem
+ * whose 256x256 tiles fill whole rounds of the CUs plus a small ragged
+ * round.  *nsplit > 0: output columns [0, nsplit) run as 256x256 tiles and
+ * [nsplit, N) as a second launch with the table's choice for that shape;
+ * *nsplit < 0: the same with rows [0, -nsplit) and [-nsplit, M); 0: one
+ * grid.  No counterpart in the reference (one Triton grid per call);
+ * exposed for host-side checks.
  */
 int f16acc_tail_split(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
                       const void* a, const void* b, int64_t* nsplit);

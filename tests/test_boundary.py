@@ -193,6 +193,9 @@ def test_patch_enable_disable_and_cpu_fallback():
     (4096, 4096, 4096, 0),      # whole rounds
     (2048, 151936, 1536, 0),    # lm_head: the ragged round is half full, a tail gains < 3 %
     (2048, 1536, 1536, 0),      # under one round
+    (8960, 2048, 1536, -8192),  # tall: the row cut fills the first round, the column cut would not
+    (8960, 4096, 1536, -8192),  # only the row cut gains
+    (4096, 8960, 1536, 8192),   # only the column cut gains
 ])
 def test_ragged_round_tail_plan(M, N, K, want):
     """Where f16acc_gemm cuts a ragged last 256x256 round into a second launch

@@ -563,3 +563,37 @@ def test_randomized_shapes_layouts_and_tiles_match_oracle(case):
         assert err < TOL, (case, M, N, K, tile, out_dtype, chunked, float(err))
     else:
         assert torch.equal(c.cpu()[finite], ref[finite])
+
+
+@pytest.mark.parametrize("b_layout", ["w.t()", "row-major"])
+def test_ragged_round_row_cut_equals_single_grid(b_layout):
+    """A tall problem (8960 x 2048 x 1536: 35 x 8 tiles of 256x256 for 256
+    CUs) is cut along M: rows 0..8191 as one round of 256x256 tiles, the last
+    768 as a second launch (a offset by 8192 rows, c by 8192 rows).  Every
+    element is computed as in the single grid, bit for bit; the fused bias
+    is per column, so it applies unchanged to both launches."""
+    from f16acc_amd import patch
+
+    x, w, bias = rnd((8960, 1536), 110), rnd((2048, 1536), 111, 0.05), rnd((2048,), 112, 0.5)
+    gx = x.cuda()
+    gb = w.cuda().t() if b_layout == "w.t()" else w.t().contiguous().cuda()
+    assert _tail_split(gx, gb) == -8192
+    c = f16acc.mm(gx, gb)
+    c1, flags = mm_flags(gx, gb)
+    assert int(flags.sum()) == 0
+    assert torch.equal(c, c1)
+    assert rel(c.cpu(), chunk32.mm(x, w.t(), torch.float16, tile=(128, 128))) < TOL
+    if b_layout == "w.t()":
+        unfused = c.clone()
+        unfused += bias.cuda()
+        with torch.no_grad():
+            assert torch.equal(patch.linear(gx, w.cuda(), bias.cuda()), unfused)
+    # the forced-overflow closed form in the first and in the second launch
+    xo, wo = x.clone(), w.clone()
+    for r0 in (300, 8500):
+        xo[r0 : r0 + 10, :] = 100.0
+    wo[40:50, :] = 0.0
+    wo[40:50, 0:32], wo[40:50, 32:64], wo[40:50, 64:96], wo[40:50, 96:128] = 30.0, -30.0, 30.0, -30.0
+    wo[40:50, 127] = -29.0
+    co = f16acc.mm(xo.cuda(), wo.cuda().t(), torch.float32)
+    assert torch.all(co[300:310, 40:50] == 100.0) and torch.all(co[8500:8510, 40:50] == 100.0)
