@@ -127,9 +127,13 @@ __device__ __forceinline__ int nc_swz(int krow) { return 2 * (krow & 3) + 8 * ((
 // Layout of B in LDS.
 enum BLayout { kKC = 0, kNC = 1 };
 
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int NS_, int BL_>
+// WPE: waves per SIMD the kernel is compiled for (amdgpu_waves_per_eu): 2
+// caps a wave at 256 registers, 4 at 128 (the 64x64 tile runs four
+// workgroups of four waves per CU).
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int NS_, int BL_, int WPE_ = 2>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, NS = NS_, BL = BL_;
+  static constexpr int WPE = WPE_;
   static constexpr int T = 64 * WAVES_M * WAVES_N;
   static constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;  // wave tile
   static constexpr int FM = WTM / 16, FN = WTN / 16;            // 16x16 MFMA blocks per wave
@@ -440,7 +444,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
   constexpr bool kSpread = T >= 32;
   constexpr int kDmaEvery = T / (2 * kUnits) > 0 ? T / (2 * kUnits) : 1;
   if (!kSpread && has_next) next.all();
-  // Tiles of 4-wave workgroups run two or three workgroups per CU, so a
+  // Tiles of 4-wave workgroups run two or four workgroups per CU, so a
   // SIMD's waves belong to workgroups in different phases: raising the
   // priority of a wave in its MFMA loop over one in its barrier and copy
   // phase measured +1.3-4.9 % on 128x128 (none on the 8-wave tiles, whose
@@ -702,12 +706,12 @@ __device__ __forceinline__ int part_offset(int i, int j, int tid) {
 }
 
 // Whole-K (kWhole) and split-K partial (kPartial) kernel; FAST selects the
-// direct-to-LDS loader.  amdgpu_waves_per_eu(2) caps a wave at 256
-// registers, which keeps every MFMA in its VGPR form: the chunk partials are
-// read by VALU conversions, and an AGPR destination would cost a
-// v_accvgpr_read per register.
+// direct-to-LDS loader.  amdgpu_waves_per_eu(C::WPE >= 2) caps a wave at 256
+// registers or fewer, which keeps every MFMA in its VGPR form: the chunk
+// partials are read by VALU conversions, and an AGPR destination would cost
+// a v_accvgpr_read per register.
 template <class C, bool FAST, bool CHUNKED, bool OUT32>
-__global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(Params p) {
+__global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) void gemm_kernel(Params p) {
   __shared__ __attribute__((aligned(1024))) char smem_raw[FAST ? C::NS * C::STAGE : C::STAGE];
   __shared__ int tile_bad;
   char LDS_AS* smem = (char LDS_AS*)smem_raw;
@@ -837,12 +841,12 @@ __global__ __launch_bounds__(256) void pack_kernel(const f16* __restrict__ src, 
 //   2   128x256  8      64x64      3 x 48 KiB    1
 //   3   128x128  4      64x64      2 x 32 KiB    2
 //   4   128x128  4      64x64      1 x 32 KiB    generic strided gather path
-//   5   64x64    4      32x32      3 x 16 KiB    3
+//   5   64x64    4      32x32      2 x 16 KiB    4
 template <int BL> using Cfg0 = Cfg<256, 256, 4, 2, 2, BL>;
 template <int BL> using Cfg1 = Cfg<256, 128, 4, 2, 3, BL>;
 template <int BL> using Cfg2 = Cfg<128, 256, 2, 4, 3, BL>;
 template <int BL> using Cfg3 = Cfg<128, 128, 2, 2, 2, BL>;
-template <int BL> using Cfg5 = Cfg<64, 64, 2, 2, 3, BL>;
+template <int BL> using Cfg5 = Cfg<64, 64, 2, 2, 2, BL, 4>;
 using CfgG = Cfg<128, 128, 2, 2, 2, kKC>;
 
 struct TileInfo {
@@ -850,7 +854,7 @@ struct TileInfo {
 };
 constexpr TileInfo kTiles[F16ACC_NUM_TILES] = {
     {256, 256, 512, 1}, {256, 128, 512, 1}, {128, 256, 512, 1}, {128, 128, 256, 2}, {128, 128, 256, 2},
-    {64, 64, 256, 3}};
+    {64, 64, 256, 4}};
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -894,14 +898,15 @@ constexpr double kTileRate[4] = {1.00, 0.87, 0.87, 0.89};
 //   estimated time = ceil(tiles / (CUs x per_cu)) x tile area x per_cu / rate
 // where the pick may also split K (plan_split; the split's own estimate
 // divides by the split count and adds kSplitCost for the second launch and
-// the partials' traffic).  64x64 runs three workgroups per CU, each wave
-// 32x32: it reads twice the LDS per MFMA of a 64x64 wave tile (rate 0.65),
-// but four times the tiles fill the GPU.  Measured: Qwen2.5-1.5B k/v
-// 2048x256x1536 20.0 -> 11.3 us and q/o 2048x1536x1536 21.6 -> 19.7 us
-// against 128x128; down 2048x1536x8960 92-96 us, as fast as 128x128 split
-// in two and in one launch; gate/up 2048x8960x1536 stays off 64x64 (101 us
-// against 83.6 us on 128x128).
-constexpr double kSmallTileRate = 0.65;
+// the partials' traffic).  64x64 runs four workgroups per CU (two-stage
+// ring, 128 registers), each wave 32x32: it reads twice the LDS per MFMA of
+// a 64x64 wave tile (rate 0.70), but four times the tiles fill the GPU.
+// Measured: Qwen2.5-1.5B k/v 2048x256x1536 20.0 -> 10.5 us and q/o
+// 2048x1536x1536 21.6 -> 17.4 us against 128x128; long K keeps the 128x128
+// split (down 2048x1536x8960 84.1 us against 89.9 on 64x64, the packed
+// 2049x1537x8968 config 97.5 against 111.1); gate/up 2048x8960x1536 stays
+// off 64x64 (101 us against 83.6 us on 128x128).
+constexpr double kSmallTileRate = 0.70;
 constexpr double kSplitCost = 1.08;
 constexpr int kMinSplitStages = 16;
 constexpr int kMaxSplits = 16;

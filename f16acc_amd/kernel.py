@@ -128,31 +128,35 @@ def _pack(src, rows, cols, s_r, s_c, ld):
 
 
 def _pack_plan(a, b, M, N, K, tile=None):
-    """(pack_a, pack_b, Kp): which operands mm copies before the GEMM, and the
-    K it then runs with.  Nothing is packed when the fast kernels can read a
-    and b directly, when the problem is too small to repay a copy, or when the
-    generic tile is forced; otherwise K is padded to a multiple of 8 by zeros
-    and every operand that is not fast (or all, when K changes) is packed."""
+    """(pack_a, pack_b, Kp, ld): which operands mm copies before the GEMM, the
+    K it then runs with, and the row length of the copies.  Nothing is packed
+    when the fast kernels can read a and b directly, when the problem is too
+    small to repay a copy, or when the generic tile is forced; otherwise K is
+    padded to a multiple of 8 by zeros and every operand that is not fast (or
+    all, when K changes) is packed.  The copies' rows are ld = K rounded up to
+    64 elements long, so that every row starts on a 128-byte cache line (rows
+    of 8968 halves straddle lines and doubled the GEMM's memory transactions
+    on the 2049 x 1537 x 8961 config)."""
     if K == 0 or tile == "generic" or (tile is None and M * N * K < PACK_MIN_MACS):
-        return False, False, K
+        return False, False, K, K
     ok_a, ok_b = _fast_a(a, K), _fast_b(b, K, N)
     if ok_a and ok_b:
-        return False, False, K
+        return False, False, K, K
     Kp = -(-K // 8) * 8
-    return Kp != K or not ok_a, Kp != K or not ok_b, Kp
+    return Kp != K or not ok_a, Kp != K or not ok_b, Kp, -(-K // 64) * 64
 
 
 def _operands(a, b, M, N, K, tile=None):
-    """The operands the GEMM runs on (see _pack_plan): a as [M, Kp] rows, b as
-    the K-contiguous [Kp, N] view of an [N, Kp] buffer when packed.
-    Returns (a, b, K) for the launch."""
-    pack_a, pack_b, Kp = _pack_plan(a, b, M, N, K, tile)
+    """The operands the GEMM runs on (see _pack_plan): a as the [M, Kp] view
+    of an [M, ld] buffer, b as the K-contiguous [Kp, N] view of an [N, ld]
+    buffer when packed.  Returns (a, b, K) for the launch."""
+    pack_a, pack_b, Kp, ld = _pack_plan(a, b, M, N, K, tile)
     if pack_a:
         with torch.cuda.device(a.device):
-            a = _pack(a, M, K, a.stride(0), a.stride(1), Kp)
+            a = _pack(a, M, K, a.stride(0), a.stride(1), ld)[:, :Kp]
     if pack_b:
         with torch.cuda.device(b.device):
-            b = _pack(b, N, K, b.stride(1), b.stride(0), Kp).t()  # element (n, k) = b[k][n]
+            b = _pack(b, N, K, b.stride(1), b.stride(0), ld)[:, :Kp].t()  # element (n, k) = b[k][n]
     return a, b, Kp
 
 
@@ -204,9 +208,9 @@ def tile_config(a, b, tile=None):
     of Kp elements)."""
     M, K = a.shape
     N = b.shape[1]
-    pack_a, pack_b, Kp = _pack_plan(a, b, M, N, K, tile) if M and N else (False, False, K)
-    sam, sak, pa = (Kp, 1, 0) if pack_a else (a.stride(0), a.stride(1), a.data_ptr())
-    sbk, sbn, pb = (1, Kp, 0) if pack_b else (b.stride(0), b.stride(1), b.data_ptr())
+    pack_a, pack_b, Kp, ld = _pack_plan(a, b, M, N, K, tile) if M and N else (False, False, K, K)
+    sam, sak, pa = (ld, 1, 0) if pack_a else (a.stride(0), a.stride(1), a.data_ptr())
+    sbk, sbn, pb = (1, ld, 0) if pack_b else (b.stride(0), b.stride(1), b.data_ptr())
     tid, bm, bn, fam, thr = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     tm, tn = ctypes.c_int64(), ctypes.c_int64()
     _lib.check(_lib.tile_config(M, N, Kp, sam, sak, sbk, sbn, pa, pb, _tile_id(tile), ctypes.byref(tid),

@@ -31,7 +31,7 @@ extern "C" {
 #define F16ACC_TILE_128x256 2
 #define F16ACC_TILE_128x128 3
 #define F16ACC_TILE_GENERIC 4 /* 128x128, any strides, element gather */
-#define F16ACC_TILE_64x64 5   /* small grids: 4 waves of 32x32, 3 workgroups per CU */
+#define F16ACC_TILE_64x64 5   /* small grids: 4 waves of 32x32, 4 workgroups per CU */
 #define F16ACC_NUM_TILES 6
 
 #define F16ACC_FAMILY_FAST 0    /* direct global -> LDS copies of 16-byte units */

@@ -109,7 +109,7 @@ class _Fake:
     (2048, 8960, 1536, (1536, 1), (1, 1536), "fast", "128x128"),   # 280 256-tiles: ragged 2nd wave
     (2048, 1536, 1536, (1536, 1), (1, 1536), "fast", "64x64"),     # 192 128-tiles for 512 slots, K short
     (2048, 256, 1536, (1536, 1), (1, 1536), "fast", "64x64"),      # Qwen k/v: 32 128-tiles
-    (2048, 1536, 8960, (8960, 1), (1, 8960), "fast", "64x64"),     # 192 128-tiles: 64x64 beats a K split
+    (2048, 1536, 8960, (8960, 1), (1, 8960), "fast", "128x128"),   # 192 128-tiles, long K: split in two
     (128, 1536, 1536, (1536, 1), (1536, 1), "fast", "64x64"),      # 128 rows, row-major b
     (2049, 1537, 8961, (8961, 1), (1, 8961), "fast", "128x128"),   # rows not 16-byte aligned: packed first
     (300, 1537, 8961, (8961, 1), (1, 8961), "fast", "128x128"),    # packed; K long enough to split

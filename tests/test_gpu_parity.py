@@ -206,6 +206,11 @@ def test_packed_operands_match_oracle(case):
         ga, gb = abig.cuda()[:, ::2], bbig.cuda()[:, 1::3]
     a2, b2, K2, fast = _packed_case(ga, gb)
     assert fast and K2 % 8 == 0 and K2 - a.shape[1] < 8
+    # packed copies start every row on a 128-byte line
+    if a2.data_ptr() != ga.data_ptr():
+        assert a2.stride(0) % 64 == 0 and a2.data_ptr() % 128 == 0
+    if b2.data_ptr() != gb.data_ptr():
+        assert b2.stride(1) % 64 == 0 and b2.data_ptr() % 128 == 0
     cfg = tile_config(a2, b2)
     for out_dtype in (torch.float32, torch.float16):
         c, flags = mm_flags(ga, gb, out_dtype)
