@@ -208,7 +208,7 @@ struct FastLoader {
   int b_off[C::LB];
   int b_k[C::LB];     // KC: first k of the unit; NC: k-row of the unit
 
-  __device__ void init(const Params& p, int64_t m0, int64_t n0, int tid) {
+  __device__ __forceinline__ void init(const Params& p, int64_t m0, int64_t n0, int tid) {
 #pragma unroll
     for (int j = 0; j < C::LA; ++j) {
       const int s = j * C::T + tid, row = s >> 3, u = (s & 7) ^ kc_swz(row);
@@ -249,7 +249,7 @@ struct FastLoader {
     }
   };
 
-  __device__ Stage stage(const Params& p, int64_t m0, int64_t n0, int64_t kbase, int64_t kend, char LDS_AS* slot,
+  __device__ __forceinline__ Stage stage(const Params& p, int64_t m0, int64_t n0, int64_t kbase, int64_t kend, char LDS_AS* slot,
                          int wave) const {
     Stage st;
     const int64_t krem = kend - kbase;  // k < krem is inside this workgroup's K range
@@ -262,7 +262,7 @@ struct FastLoader {
   }
 
   // Issue all global -> LDS copies of the stage starting at k = kbase.
-  __device__ void issue(const Params& p, int64_t m0, int64_t n0, int64_t kbase, int64_t kend, char LDS_AS* slot,
+  __device__ __forceinline__ void issue(const Params& p, int64_t m0, int64_t n0, int64_t kbase, int64_t kend, char LDS_AS* slot,
                         int wave) const {
     stage(p, m0, n0, kbase, kend, slot, wave).all();
   }
