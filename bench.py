@@ -200,6 +200,7 @@ def shapes_report(names, rounds=4):
     from f16acc_amd.kernel import tile_config
 
     torch.backends.cuda.matmul.allow_fp16_reduced_precision_reduction = False
+    torch.backends.cuda.preferred_blas_library("hipblaslt")
     rows = []
     for name in names:
         M, N, K, layout, out_dtype = WORKLOADS[name]
@@ -450,6 +451,7 @@ def main():
     from f16acc_amd.kernel import tile_config
 
     torch.backends.cuda.matmul.allow_fp16_reduced_precision_reduction = False
+    torch.backends.cuda.preferred_blas_library("hipblaslt")
     M, N, K, layout, out_dtype = WORKLOADS[args.workload]
     a_cpu, b_cpu, a, b = make_inputs(M, N, K, layout)
     flops = 2.0 * M * N * K

@@ -561,6 +561,10 @@ __device__ __forceinline__ void k_loop_generic(const Params& p, int64_t m0, int6
   if (CHUNKED && nsteps > 0) pipe_drain<C>(pp, lane, acc);
 }
 
+// 16 bytes at any even address: gfx950 global loads and stores allow any
+// alignment (a misaligned unit costs a second cache line, not a fault).
+typedef f16x8 __attribute__((aligned(2))) f16x8_a2;
+
 // Output value of one element.  With a bias the epilogue reproduces the
 // reference's unfused sequence (f16acc/patch.py:28-30: y = mm(...) in fp16,
 // then y += b, which torch evaluates as fp16(float(y) + float(b))): the FP32
@@ -573,13 +577,17 @@ __device__ __forceinline__ float with_bias(float v, const f16* bias, int64_t col
   return OUT32 ? v + b : (float)(f16)v + b;
 }
 
-// fp16 output of a tile that lies wholly inside c, staged through LDS so
-// that every lane stores 16 contiguous bytes and a row leaves as whole cache
-// lines: the MFMA layout alone gives 8-byte stores covering 32 bytes of a
-// row per instruction, which reached HBM as partial lines (about twice the
-// output's bytes written, by rocprofv3 WRITE_SIZE).  Each wave stages its
-// own WTM x WTN sub-tile in its own LDS slice (the LDS is free once the K
-// loop's final barrier has passed), 16-byte units XOR-swizzled by row.
+// fp16 output of a tile, staged through LDS so that every lane stores 16
+// contiguous bytes and a row leaves as whole cache lines: the MFMA layout
+// alone gives 8-byte stores covering 32 bytes of a row per instruction,
+// which reached HBM as partial lines (about twice the output's bytes
+// written, by rocprofv3 WRITE_SIZE).  Each wave stages its own WTM x WTN
+// sub-tile in its own LDS slice (the LDS is free once the K loop's final
+// barrier has passed), 16-byte units XOR-swizzled by row.  Needs rows of c
+// contiguous (scn == 1).  Rows that are not 16-byte aligned (N = 1537) take
+// 16-byte stores at their 2-byte aligned addresses, and units at the edge
+// of c are stored element by element, so edge tiles and odd N stay on this
+// path instead of one 2-byte store per element and lane.
 template <class C>
 __device__ __forceinline__ void store_tile_staged(const Params& p, int64_t m0, int64_t n0, int wm, int wn, int lane,
                                                   int wave, char LDS_AS* smem, const f32x4 (&acc)[C::FM][C::FN]) {
@@ -597,7 +605,10 @@ __device__ __forceinline__ void store_tile_staged(const Params& p, int64_t m0, i
       f32x4 v = acc[i][j];
       if (p.bias) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = with_bias<false>(v[r], p.bias, col0 + 16 * j + 4 * g + r);
+        for (int r = 0; r < 4; ++r) {
+          const int64_t col = col0 + 16 * j + 4 * g + r;
+          if (col < p.N) v[r] = with_bias<false>(v[r], p.bias, col);
+        }
       }
       const f32x2 lo = {v[0], v[1]}, hi = {v[2], v[3]};
       const f16x2 hl = __builtin_convertvector(lo, f16x2), hh = __builtin_convertvector(hi, f16x2);
@@ -607,11 +618,24 @@ __device__ __forceinline__ void store_tile_staged(const Params& p, int64_t m0, i
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
   __builtin_amdgcn_wave_barrier();
   f16* cbase = (f16*)p.c + (m0 + wm * C::WTM) * p.scm + col0;
+  const int64_t rows_in = p.M - (m0 + wm * C::WTM), cols_in = p.N - col0;  // of this wave's sub-tile
+  const bool whole = p.vec_store && rows_in >= C::WTM && cols_in >= C::WTN;
 #pragma unroll
   for (int it = 0; it < C::WTM * U / 64; ++it) {
     const int idx = it * 64 + lane, row = idx / U, u = idx % U;
     const f16x8 v = *(const f16x8 LDS_AS*)(w + row * ROW + ((u ^ (row % U)) << 4));
-    *(f16x8*)(cbase + row * p.scm + 8 * u) = v;
+    if (whole) {
+      *(f16x8*)(cbase + row * p.scm + 8 * u) = v;
+    } else if (row < rows_in) {
+      f16* dst = cbase + row * p.scm + 8 * u;
+      if (8 * u + 8 <= cols_in) {
+        *(f16x8_a2*)dst = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (8 * u + e < cols_in) dst[e] = v[e];
+      }
+    }
   }
 }
 
@@ -689,7 +713,7 @@ __device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, 
         k_loop_generic<C, false>(p, m0, n0, smem, tid, wm, wn, lane, acc);
     }
   }
-  if (!OUT32 && C::BM * C::BN * 2 <= SMEM && p.vec_store && m0 + C::BM <= p.M && n0 + C::BN <= p.N)
+  if (!OUT32 && C::BM * C::BN * 2 <= SMEM && p.scn == 1)
     store_tile_staged<C>(p, m0, n0, wm, wn, lane, wave, smem, acc);
   else
     store_tile<C, OUT32>(p, m0, n0, wm, wn, lane, acc);
@@ -808,11 +832,15 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void 
 // dst[r][c] = src[r * s_r + c * s_c] for r < rows, c < cols, and 0 in the
 // padding up to rows_pad x ld.  Zero padding along K adds exact zeros to the
 // last chunk's sum, so the chunk semantics are unchanged.  One thread writes
-// one 16-byte unit; consecutive threads read consecutive source elements
-// when s_c == 1.  A transposing copy (s_r == 1: a row-major b packed into
-// the K-contiguous layout) numbers the units column-major instead, so that
+// one 16-byte unit.  With s_c == 1 (rows contiguous, as for K = 8961) a
+// whole unit inside the row is one 16-byte load at its 2-byte aligned
+// address (gfx950 global loads allow any alignment; element loads ran at
+// about half the HBM rate), and consecutive threads read consecutive
+// units.  A transposing copy (s_r == 1: a row-major b packed into the
+// K-contiguous layout) numbers the units column-major instead, so that
 // consecutive threads read consecutive source elements there too.
 // ---------------------------------------------------------------------------
+
 template <bool COLUMN_MAJOR_UNITS>
 __global__ __launch_bounds__(256) void pack_kernel(const f16* __restrict__ src, f16* __restrict__ dst,
                                                   int64_t rows, int64_t cols, int64_t s_r, int64_t s_c,
@@ -823,10 +851,14 @@ __global__ __launch_bounds__(256) void pack_kernel(const f16* __restrict__ src, 
   const int64_t r = COLUMN_MAJOR_UNITS ? u % rows_pad : u / units_per_row;
   const int64_t c0 = 8 * (COLUMN_MAJOR_UNITS ? u / rows_pad : u % units_per_row);
   f16x8 v;
+  if (!COLUMN_MAJOR_UNITS && s_c == 1 && r < rows && c0 + 8 <= cols) {
+    v = *(const f16x8_a2*)(src + r * s_r + c0);
+  } else {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int64_t c = c0 + e;
-    v[e] = (r < rows && c < cols) ? src[r * s_r + c * s_c] : (f16)0.0f;
+    for (int e = 0; e < 8; ++e) {
+      const int64_t c = c0 + e;
+      v[e] = (r < rows && c < cols) ? src[r * s_r + c * s_c] : (f16)0.0f;
+    }
   }
   *(f16x8*)(dst + r * ld + c0) = v;
 }

@@ -148,6 +148,28 @@ def test_every_tile_matches_oracle(tile, K):
 
 
 @pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic", "64x64"])
+def test_every_tile_stores_unaligned_rows_and_edges(tile):
+    """fp16 rows of N = 517 halves start off 16-byte alignment, and M, N leave
+    partial tiles: such tiles are staged through LDS and leave as 16-byte
+    units at 2-byte aligned addresses, element by element at the edge.  The
+    FP32 sums do not depend on the output dtype, so the fp16 output must be
+    the fp32 output of the same tile rounded to fp16, bit for bit."""
+    from f16acc_amd.kernel import mm_tile
+
+    M, N, K = 300, 517, 200
+    a, b = rnd((M, K), 30), rnd((K, N), 31)
+    ga = a.cuda()
+    for b_t in (False, True):
+        gb = b.t().contiguous().cuda().t() if b_t else b.cuda()
+        for chunked in (True, False):
+            c16 = mm_tile(ga, gb, tile, torch.float16, chunked=chunked)
+            c32 = mm_tile(ga, gb, tile, torch.float32, chunked=chunked)
+            assert torch.equal(c16, c32.half()), (tile, b_t, chunked)
+        ref, _ = oracle(a, b, torch.float16, tile_config(ga, gb, tile))
+        assert rel(c16.cpu(), ref) < TOL
+
+
+@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic", "64x64"])
 def test_every_tile_redoes_overflowing_tiles(tile):
     """Overflow closed form (reference tests/test_f16acc.py:91-101) placed in
     one tile of a larger grid: that tile is flagged and exact, the others not."""
@@ -262,7 +284,8 @@ def test_overflow_stress_flags_exactly_the_block_intersections():
     assert rel(c.cpu()[~mask.cpu()], ref[~mask.cpu()]) < TOL
 
 
-@pytest.mark.parametrize("shape", [(256, 384, 640), (300, 1000, 77), (1024, 1536, 256), (128, 0, 16)])
+@pytest.mark.parametrize("shape", [(256, 384, 640), (300, 1000, 77), (300, 200, 517), (1024, 1536, 256),
+                                   (128, 0, 16)])
 def test_fused_bias_equals_unfused_add_bit_for_bit(shape):
     """The patched nn.Linear adds its bias in the GEMM's store; the result must
     equal the reference's unfused y = mm(x2, w.t()); y += b exactly
