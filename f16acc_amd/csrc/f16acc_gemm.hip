@@ -49,6 +49,9 @@ namespace {
 
 typedef _Float16 f16;
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+// 16 bytes at any even address: gfx950 global loads and stores allow any
+// alignment (a misaligned unit costs a second cache line, not a fault).
+typedef f16x8 __attribute__((aligned(2))) f16x8_a2;
 typedef f16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -126,6 +129,12 @@ __device__ __forceinline__ int nc_swz(int krow) { return 2 * (krow & 3) + 8 * ((
 
 // Layout of B in LDS.
 enum BLayout { kKC = 0, kNC = 1 };
+
+// How a kernel fills its LDS stages: kGather, element gathers through
+// registers (any strides); kDma, 16-byte global -> LDS copies (rows 16-byte
+// aligned); kReg, 16-byte loads at any even address into registers, then
+// LDS stores (unit-stride rows of any alignment and length).
+enum Loader { kGather = 0, kDma = 1, kReg = 2 };
 
 // WPE: waves per SIMD the kernel is compiled for (amdgpu_waves_per_eu): 2
 // caps a wave at 256 registers, 4 at 128 (the 64x64 tile runs four
@@ -515,6 +524,117 @@ __device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t
   __syncthreads();  // LDS free for a redo pass
 }
 
+// ---------------------------------------------------------------------------
+// Register-staged loader (kReg): the operands' rows are unit-stride but may
+// start at any even address and end anywhere (K = 8961, offset views, a
+// row-major b with odd N), which the direct-to-LDS copies cannot read.  Each
+// thread fills the same 16-byte LDS units as FastLoader, in the same swizzled
+// layouts, with one 16-byte global load at the unit's 2-byte aligned address;
+// a unit that crosses the end of K (or of N for a row-major b) is read
+// element by element, and units past the end read nothing (zeros, as the
+// reference's masked loads, f16acc/kernel.py:45-47).  The loads of stage
+// s + 1 are in flight while stage s is multiplied; their LDS stores follow.
+// ---------------------------------------------------------------------------
+template <class C>
+struct RegLoader {
+  // Unit j of a thread sits j * T / 8 rows (KC) or j * T / UB k-rows (NC)
+  // below its unit 0, at the same swizzled column: the swizzles repeat every
+  // 16 rows and T / 8, T / UB are multiples of 16.  So a thread keeps only
+  // its unit 0.
+  static constexpr int RA = C::T / 8, RB = C::BL == kKC ? C::T / 8 : C::T / C::UB;
+  static_assert(RA % 16 == 0 && RB % 16 == 0, "unit rows must keep the swizzle phase");
+  int a_row, a_k;  // unit 0 of A: tile row, first k in the stage
+  int b_row, b_k;  // unit 0 of B: KC tile column and first k; NC k-row and first column
+
+  __device__ __forceinline__ void init(int tid) {
+    a_row = tid >> 3;
+    a_k = 8 * ((tid & 7) ^ kc_swz(a_row));
+    if (C::BL == kKC) {
+      b_row = tid >> 3;
+      b_k = 8 * ((tid & 7) ^ kc_swz(b_row));
+    } else {
+      b_row = tid / C::UB;
+      b_k = 8 * ((tid % C::UB) ^ (nc_swz(b_row) & (C::UB - 1)));
+    }
+  }
+
+  // the n valid elements (n <= 8) of a unit at w, zeros after them
+  static __device__ __forceinline__ f16x8 unit(const f16* w, int64_t n) {
+    f16x8 v = {};
+    if (n >= 8) {
+      v = *(const f16x8_a2*)w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (e < n) v[e] = w[e];
+    }
+    return v;
+  }
+
+  // Loads of the stage starting at k = kbase (k < kend is this workgroup's range).
+  __device__ __forceinline__ void load(const Params& p, int64_t m0, int64_t n0, int64_t kbase, int64_t kend,
+                                       f16x8 (&buf)[C::LA + C::LB]) const {
+    const int64_t krem = kend - kbase;
+    const f16* wa = p.a + (m0 + a_row) * p.sam + kbase + a_k;
+#pragma unroll
+    for (int j = 0; j < C::LA; ++j) {
+      buf[j] = f16x8{};
+      if (m0 + a_row + j * RA < p.M && a_k < krem) buf[j] = unit(wa + (int64_t)j * RA * p.sam, krem - a_k);
+    }
+#pragma unroll
+    for (int j = 0; j < C::LB; ++j) {
+      buf[C::LA + j] = f16x8{};
+      if (C::BL == kKC) {
+        const f16* wb = p.b + (n0 + b_row) * p.sbn + kbase + b_k;
+        if (n0 + b_row + j * RB < p.N && b_k < krem) buf[C::LA + j] = unit(wb + (int64_t)j * RB * p.sbn, krem - b_k);
+      } else {
+        const f16* wb = p.b + (kbase + b_row) * p.sbk + n0 + b_k;
+        const int64_t nrem = p.N - (n0 + b_k);
+        if (b_row + j * RB < krem && nrem > 0) buf[C::LA + j] = unit(wb + (int64_t)j * RB * p.sbk, nrem);
+      }
+    }
+  }
+
+  // LDS stores of loaded units into the stage at `slot`: unit j of thread
+  // tid goes where FastLoader's copy of it lands.
+  static __device__ __forceinline__ void store(const f16x8 (&buf)[C::LA + C::LB], char LDS_AS* slot, int tid) {
+#pragma unroll
+    for (int j = 0; j < C::LA; ++j) *(f16x8 LDS_AS*)(slot + (j * C::T + tid) * 16) = buf[j];
+#pragma unroll
+    for (int j = 0; j < C::LB; ++j) *(f16x8 LDS_AS*)(slot + C::A_STAGE + (j * C::T + tid) * 16) = buf[C::LA + j];
+  }
+};
+
+// K loop of the kReg path: stage s + 1's loads are issued before stage s is
+// multiplied and stored into the other slot after it; one barrier per stage
+// publishes the stores and retires every wave's reads of the slot the next
+// stores overwrite.
+template <class C, bool CHUNKED>
+__device__ __forceinline__ void k_loop_reg(const Params& p, int64_t m0, int64_t n0, int64_t kbeg, int64_t kend,
+                                           char LDS_AS* smem, const RegLoader<C>& rl, int tid, int wm, int wn,
+                                           int lane, f32x4 (&acc)[C::FM][C::FN]) {
+  static_assert(C::NS == 2, "the kReg loop alternates two LDS stages");
+  const int64_t nsteps = (kend - kbeg + kStageK - 1) / kStageK;
+  if (nsteps <= 0) return;
+  f16x8 buf[C::LA + C::LB];
+  rl.load(p, m0, n0, kbeg, kend, buf);
+  RegLoader<C>::store(buf, smem, tid);
+  if (nsteps > 1) rl.load(p, m0, n0, kbeg + kStageK, kend, buf);
+  __syncthreads();
+  Pipe<C> pp;
+  const typename FastLoader<C>::Stage none{};
+  for (int64_t s = 0; s < nsteps; ++s) {
+    char LDS_AS* cur = smem + (s & 1) * C::STAGE;
+    compute_stage<C, CHUNKED>(cur, wm, wn, lane, acc, none, false, pp);
+    if (s + 1 < nsteps) {
+      RegLoader<C>::store(buf, smem + ((s + 1) & 1) * C::STAGE, tid);
+      if (s + 2 < nsteps) rl.load(p, m0, n0, kbeg + (s + 2) * kStageK, kend, buf);
+    }
+    __syncthreads();
+  }
+  if (CHUNKED) pipe_drain<C>(pp, lane, acc);
+}
+
 // Generic path: gathers elements with any strides through registers into
 // the KC layout (both operands), one stage at a time.
 template <class C>
@@ -560,10 +680,6 @@ __device__ __forceinline__ void k_loop_generic(const Params& p, int64_t m0, int6
   }
   if (CHUNKED && nsteps > 0) pipe_drain<C>(pp, lane, acc);
 }
-
-// 16 bytes at any even address: gfx950 global loads and stores allow any
-// alignment (a misaligned unit costs a second cache line, not a fault).
-typedef f16x8 __attribute__((aligned(2))) f16x8_a2;
 
 // Output value of one element.  With a bias the epilogue reproduces the
 // reference's unfused sequence (f16acc/patch.py:28-30: y = mm(...) in fp16,
@@ -683,8 +799,8 @@ __device__ __forceinline__ void store_tile(const Params& p, int64_t m0, int64_t 
 
 // Flag, redo and store of a finished FP32 tile sum (shared by the whole-K
 // kernel and the split-K finishing kernel).
-template <class C, bool FAST, bool CHUNKED, bool OUT32, int SMEM>
-__device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, FastLoader<C>& ld, int* tile_bad,
+template <class C, int LD, bool CHUNKED, bool OUT32, int SMEM>
+__device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, FastLoader<C>& ld, const RegLoader<C>& rl, int* tile_bad,
                                             int64_t tm, int64_t tn, int tid, int wave, int wm, int wn, int lane,
                                             f32x4 (&acc)[C::FM][C::FN]) {
   const int64_t m0 = tm * C::BM, n0 = tn * C::BN;
@@ -707,8 +823,10 @@ __device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, 
       for (int i = 0; i < C::FM; ++i)
 #pragma unroll
         for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (FAST)
+      if constexpr (LD == kDma)
         k_loop_fast<C, false>(p, m0, n0, 0, p.K, smem, ld, wave, wm, wn, lane, acc);
+      else if constexpr (LD == kReg)
+        k_loop_reg<C, false>(p, m0, n0, 0, p.K, smem, rl, tid, wm, wn, lane, acc);
       else
         k_loop_generic<C, false>(p, m0, n0, smem, tid, wm, wn, lane, acc);
     }
@@ -729,14 +847,15 @@ __device__ __forceinline__ int part_offset(int i, int j, int tid) {
   return ((i * C::FN + j) * C::T + tid) * 4;
 }
 
-// Whole-K (kWhole) and split-K partial (kPartial) kernel; FAST selects the
-// direct-to-LDS loader.  amdgpu_waves_per_eu(C::WPE >= 2) caps a wave at 256
+// Whole-K (kWhole) and split-K partial (kPartial) kernel; LD is the stage
+// loader (Loader).  amdgpu_waves_per_eu(C::WPE >= 2) caps a wave at 256
 // registers or fewer, which keeps every MFMA in its VGPR form: the chunk
 // partials are read by VALU conversions, and an AGPR destination would cost
 // a v_accvgpr_read per register.
-template <class C, bool FAST, bool CHUNKED, bool OUT32>
+template <class C, int LD, bool CHUNKED, bool OUT32>
 __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) void gemm_kernel(Params p) {
-  __shared__ __attribute__((aligned(1024))) char smem_raw[FAST ? C::NS * C::STAGE : C::STAGE];
+  constexpr int kSmem = LD == kGather ? C::STAGE : C::NS * C::STAGE;
+  __shared__ __attribute__((aligned(1024))) char smem_raw[kSmem];
   __shared__ int tile_bad;
   char LDS_AS* smem = (char LDS_AS*)smem_raw;
 
@@ -764,9 +883,13 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) 
     for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   FastLoader<C> ld;
-  if (FAST) {
+  RegLoader<C> rl;
+  if constexpr (LD == kDma) {
     ld.init(p, m0, n0, tid);
     k_loop_fast<C, CHUNKED>(p, m0, n0, kbeg, kend, smem, ld, wave, wm, wn, lane, acc);
+  } else if constexpr (LD == kReg) {
+    rl.init(tid);
+    k_loop_reg<C, CHUNKED>(p, m0, n0, kbeg, kend, smem, rl, tid, wm, wn, lane, acc);
   } else {
     k_loop_generic<C, CHUNKED>(p, m0, n0, smem, tid, wm, wn, lane, acc);
   }
@@ -785,8 +908,7 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) 
                                                part_offset<C>(i, j, 0) * 4, 0);
     return;
   }
-  finish_tile<C, FAST, CHUNKED, OUT32, (FAST ? C::NS * C::STAGE : C::STAGE)>(p, smem, ld, &tile_bad, tm, tn, tid,
-                                                                            wave, wm, wn, lane, acc);
+  finish_tile<C, LD, CHUNKED, OUT32, kSmem>(p, smem, ld, rl, &tile_bad, tm, tn, tid, wave, wm, wn, lane, acc);
 }
 
 // Split-K finishing kernel (kFinish): one workgroup per tile adds the FP32
@@ -821,7 +943,9 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void 
       for (int j = 0; j < C::FN; ++j) acc[i][j] += *(const f32x4*)(ps + part_offset<C>(i, j, tid));
   }
   FastLoader<C> unused;
-  finish_tile<C, false, CHUNKED, OUT32, kSmem>(p, smem, unused, &tile_bad, tm, tn, tid, wave, wm, wn, lane, acc);
+  RegLoader<C> unused_rl;
+  finish_tile<C, kGather, CHUNKED, OUT32, kSmem>(p, smem, unused, unused_rl, &tile_bad, tm, tn, tid, wave, wm, wn, lane,
+                                                 acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -898,6 +1022,17 @@ inline int cu_count() {
 }
 
 // Which loader the operands allow.  blayout: kKC / kNC, or -1 for generic.
+// kReg operands: unit-stride rows at any even address (any K, any row
+// stride), with the tile's element offsets inside 32 bits.  Returns the B
+// layout, or -1.
+inline int reg_layout(int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int bm, int bn) {
+  const int64_t lim = (int64_t)1 << 31;
+  if (!((sak == 1 || K <= 1) && sam >= 0 && (int64_t)bm * sam + kStageK < lim)) return -1;
+  if ((sbk == 1 || K <= 1) && sbn >= 0 && (int64_t)bn * sbn + kStageK < lim) return kKC;
+  if ((sbn == 1 || N <= 1) && sbk >= 0 && (int64_t)kStageK * sbk + bn < lim) return kNC;
+  return -1;
+}
+
 inline int fast_layout(int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, const void* a,
                        const void* b, int bm, int bn) {
   const bool a_ok = (sak == 1 || K <= 1) && sam % 8 == 0 && ((uintptr_t)a % 16) == 0 && K % 8 == 0 &&
@@ -1052,31 +1187,43 @@ inline Choice choose(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, 
   const int id = forced_tile >= 0 ? forced_tile : choose_tile(M, N, K, cu_count());
   if (id == F16ACC_TILE_GENERIC) return Choice{id, F16ACC_FAMILY_GENERIC, kKC};
   const int bl = fast_layout(N, K, sam, sak, sbk, sbn, a, b, kTiles[id].bm, kTiles[id].bn);
-  if (bl < 0) return Choice{F16ACC_TILE_GENERIC, F16ACC_FAMILY_GENERIC, kKC};
-  return Choice{id, F16ACC_FAMILY_FAST, bl};
+  if (bl >= 0) return Choice{id, F16ACC_FAMILY_FAST, bl};
+  // Operands the copies cannot read: the tiles with registers to spare
+  // stage them through registers (kReg); the others gather elements.  The
+  // 64x64 tile has room for a K-contiguous b only (128 registers); a
+  // row-major b moves the table's 64x64 pick to 128x128.
+  int rid = id;
+  if (rid == F16ACC_TILE_64x64 && forced_tile < 0 &&
+      reg_layout(N, K, sam, sak, sbk, sbn, kTiles[rid].bm, kTiles[rid].bn) == kNC)
+    rid = F16ACC_TILE_128x128;
+  if (rid == F16ACC_TILE_128x128 || rid == F16ACC_TILE_64x64) {
+    const int rb = reg_layout(N, K, sam, sak, sbk, sbn, kTiles[rid].bm, kTiles[rid].bn);
+    if (rb >= 0 && !(rid == F16ACC_TILE_64x64 && rb == kNC)) return Choice{rid, F16ACC_FAMILY_REG, rb};
+  }
+  return Choice{F16ACC_TILE_GENERIC, F16ACC_FAMILY_GENERIC, kKC};
 }
 
-template <class C, bool FAST>
+template <class C, int LD>
 hipError_t launch_cfg(const Params& p, int out32, int chunked, hipStream_t st) {
   const dim3 grid((unsigned)(p.tiles_m * p.tiles_n * (p.mode == kPartial ? p.splits : 1))), block(C::T);
   if (chunked) {
     if (out32)
-      hipLaunchKernelGGL((gemm_kernel<C, FAST, true, true>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((gemm_kernel<C, LD, true, true>), grid, block, 0, st, p);
     else
-      hipLaunchKernelGGL((gemm_kernel<C, FAST, true, false>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((gemm_kernel<C, LD, true, false>), grid, block, 0, st, p);
   } else {
     if (out32)
-      hipLaunchKernelGGL((gemm_kernel<C, FAST, false, true>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((gemm_kernel<C, LD, false, true>), grid, block, 0, st, p);
     else
-      hipLaunchKernelGGL((gemm_kernel<C, FAST, false, false>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((gemm_kernel<C, LD, false, false>), grid, block, 0, st, p);
   }
   return hipGetLastError();
 }
 
-template <template <int> class CF>
+template <template <int> class CF, int LD = kDma>
 hipError_t launch_fast(const Params& p, int blayout, int out32, int chunked, hipStream_t st) {
-  return blayout == kKC ? launch_cfg<CF<kKC>, true>(p, out32, chunked, st)
-                        : launch_cfg<CF<kNC>, true>(p, out32, chunked, st);
+  return blayout == kKC ? launch_cfg<CF<kKC>, LD>(p, out32, chunked, st)
+                        : launch_cfg<CF<kNC>, LD>(p, out32, chunked, st);
 }
 
 template <template <int> class CF>
@@ -1112,7 +1259,7 @@ struct SplitPlan {
 inline SplitPlan plan_split(const Choice& ch, int64_t M, int64_t N, int64_t K, int cus) {
   SplitPlan sp{1, K, 0};
   // 256x256 is not SPLITTABLE; 64x64 fills the GPU with its own tiles (choose_tile)
-  if (ch.family != F16ACC_FAMILY_FAST || ch.tile == F16ACC_TILE_256x256 || ch.tile == F16ACC_TILE_64x64) return sp;
+  if (ch.family == F16ACC_FAMILY_GENERIC || ch.tile == F16ACC_TILE_256x256 || ch.tile == F16ACC_TILE_64x64) return sp;
   const TileInfo& t = kTiles[ch.tile];
   const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
   const int64_t slots = (int64_t)cus * t.per_cu;
@@ -1185,13 +1332,16 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
   const int out32 = out_dtype == F16ACC_OUT_F32;
   hipStream_t st = (hipStream_t)stream;
   auto launch = [&](const Params& q) -> int {
+    if (ch.family == F16ACC_FAMILY_REG)  // 64x64 only with a K-contiguous b (choose)
+      return ch.tile == F16ACC_TILE_64x64 ? (int)launch_cfg<Cfg5<kKC>, kReg>(q, out32, chunked, st)
+                                          : (int)launch_fast<Cfg3, kReg>(q, ch.blayout, out32, chunked, st);
     switch (ch.tile) {
       case 0: return (int)launch_fast<Cfg0>(q, ch.blayout, out32, chunked, st);
       case 1: return (int)launch_fast<Cfg1>(q, ch.blayout, out32, chunked, st);
       case 2: return (int)launch_fast<Cfg2>(q, ch.blayout, out32, chunked, st);
       case 3: return (int)launch_fast<Cfg3>(q, ch.blayout, out32, chunked, st);
       case 5: return (int)launch_fast<Cfg5>(q, ch.blayout, out32, chunked, st);
-      default: return (int)launch_cfg<CfgG, false>(q, out32, chunked, st);
+      default: return (int)launch_cfg<CfgG, kGather>(q, out32, chunked, st);
     }
   };
   int rc = launch(p);

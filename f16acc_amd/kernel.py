@@ -22,6 +22,9 @@ _OUT = {torch.float16: _lib.OUT_F16, torch.float32: _lib.OUT_F32}
 # kernel (the copy's launch and traffic are not repaid).
 PACK_MIN_MACS = 1 << 24
 
+# f16acc_tile_config's kernel families (F16ACC_FAMILY_* in include/f16acc.h)
+_FAMILIES = ("fast", "generic", "reg")
+
 # Split-K workspace for the FP32 partials, one per (device, stream): kernels
 # on one stream run one after another, so consecutive calls on a stream can
 # share it.
@@ -130,20 +133,49 @@ def _pack(src, rows, cols, s_r, s_c, ld):
 def _pack_plan(a, b, M, N, K, tile=None):
     """(pack_a, pack_b, Kp, ld): which operands mm copies before the GEMM, the
     K it then runs with, and the row length of the copies.  Nothing is packed
-    when the fast kernels can read a and b directly, when the problem is too
-    small to repay a copy, or when the generic tile is forced; otherwise K is
-    padded to a multiple of 8 by zeros and every operand that is not fast (or
-    all, when K changes) is packed.  The copies' rows are ld = K rounded up to
+    when the fast kernels can read a and b directly, when the library's
+    register-staged loader reads them as they are (unit-stride rows at any
+    even address, where the table picks 128x128 or 64x64) and that costs
+    less than the copy (_reg_beats_pack; always for a forced tile), when the
+    problem is too small to repay a copy, or when the generic tile is forced;
+    otherwise K is padded to a multiple of 8 by zeros and every operand that
+    is not fast (or all, when K changes) is packed.  The copies' rows are ld = K rounded up to
     64 elements long, so that every row starts on a 128-byte cache line (rows
     of 8968 halves straddle lines and doubled the GEMM's memory transactions
     on the 2049 x 1537 x 8961 config)."""
-    if K == 0 or tile == "generic" or (tile is None and M * N * K < PACK_MIN_MACS):
+    if K == 0 or tile == "generic":
         return False, False, K, K
     ok_a, ok_b = _fast_a(a, K), _fast_b(b, K, N)
     if ok_a and ok_b:
         return False, False, K, K
+    small = tile is None and M * N * K < PACK_MIN_MACS
+    if (small or tile is not None or _reg_beats_pack(M, N, K)) and _raw_family(a, b, M, N, K, tile) == "reg":
+        return False, False, K, K
+    if small:
+        return False, False, K, K
     Kp = -(-K // 8) * 8
     return Kp != K or not ok_a, Kp != K or not ok_b, Kp, -(-K // 64) * 64
+
+
+def _reg_beats_pack(M, N, K):
+    """Whether reading misaligned operands in place (register-staged loads:
+    the GEMM runs ~1.4x longer than on packed copies) costs less than packing
+    them (two copies of (M + N) x K halves read and written at ~6 TB/s, plus
+    ~5 us of launches).  Measured on MI355X, w.t() operands with odd K: in
+    place wins from 256^2 x 1001 (13.9 against 34.5 us per call) up to
+    2048 x 1536 x 1537 (29.2 against 33.0 us); packing wins on
+    2049 x 1537 x 8961 (115.5 against 126.4 us)."""
+    return 0.4 * 2.0 * M * N * K / 500e12 < 4.0 * (M + N) * K / 6e12 + 5e-6
+
+
+def _raw_family(a, b, M, N, K, tile):
+    """Kernel family the library picks for a and b as they are (no packing):
+    "reg" when its register-staged loader reads them directly (unit-stride
+    rows at any even address, on the 128x128 and 64x64 tiles)."""
+    fam = ctypes.c_int()
+    _lib.check(_lib.tile_config(M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1), a.data_ptr(),
+                                b.data_ptr(), _tile_id(tile), None, None, None, None, None, ctypes.byref(fam), None))
+    return _FAMILIES[fam.value]
 
 
 def _operands(a, b, M, N, K, tile=None):
@@ -217,7 +249,7 @@ def tile_config(a, b, tile=None):
                                 ctypes.byref(bm), ctypes.byref(bn), ctypes.byref(tm), ctypes.byref(tn),
                                 ctypes.byref(fam), ctypes.byref(thr)))
     return {"tile": _lib.TILES[tid.value], "bm": bm.value, "bn": bn.value, "tiles_m": tm.value,
-            "tiles_n": tn.value, "family": ("fast", "generic")[fam.value], "threads": thr.value}
+            "tiles_n": tn.value, "family": _FAMILIES[fam.value], "threads": thr.value}
 
 
 def _launch(a, b, c, flags, M, N, K, chunked, tile=-1, bias=None, ws=None):

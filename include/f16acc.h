@@ -36,6 +36,8 @@ extern "C" {
 
 #define F16ACC_FAMILY_FAST 0    /* direct global -> LDS copies of 16-byte units */
 #define F16ACC_FAMILY_GENERIC 1 /* strided element gather through registers */
+#define F16ACC_FAMILY_REG 2     /* unit-stride rows at any even address: 16-byte loads
+                                   through registers (128x128 and 64x64 tiles) */
 
 /*
  * c[M,N] = a[M,K] @ b[K,N]; a and b binary16, c binary16 or binary32.

@@ -112,7 +112,9 @@ class _Fake:
     (2048, 1536, 8960, (8960, 1), (1, 8960), "fast", "128x128"),   # 192 128-tiles, long K: split in two
     (128, 1536, 1536, (1536, 1), (1536, 1), "fast", "64x64"),      # 128 rows, row-major b
     (2049, 1537, 8961, (8961, 1), (1, 8961), "fast", "128x128"),   # rows not 16-byte aligned: packed first
-    (300, 1537, 8961, (8961, 1), (1, 8961), "fast", "128x128"),    # packed; K long enough to split
+    (300, 1537, 8961, (8961, 1), (1, 8961), "reg", "128x128"),     # read in place (cheaper than a copy)
+    (2048, 256, 1537, (1537, 1), (1, 1537), "reg", "64x64"),       # k/v shape, odd K, w.t()
+    (2048, 256, 1537, (1537, 1), (256, 1), "reg", "128x128"),      # row-major b: 64x64 has no room
     (64, 40, 24, (24, 1), (40, 1), "fast", "64x64"),               # too small to repay a copy: as given
     (300, 200, 256, (512, 2), (700, 3), "generic", "generic"),      # strided operands
 ])
@@ -141,17 +143,30 @@ def test_forced_tile_resolves(tile):
         tile_config(_Fake((4096, 1024), (1024, 1)), _Fake((1024, 2048), (2048, 1)), "32x32")
 
 
-def test_misaligned_pointer_is_packed_or_gathered():
-    # mm copies a misaligned operand into an aligned buffer when the GEMM is
-    # big enough to repay it; the library, handed the pointer itself, gathers
+def test_misaligned_pointer_is_packed_read_in_place_or_gathered():
+    # mm copies a misaligned operand into an aligned buffer when the table
+    # picks a tile without the register-staged loader (256x256 here) and the
+    # GEMM is big enough to repay the copy; the library, handed the pointer
+    # itself, gathers there
     cfg = tile_config(_Fake((4096, 4096), (4096, 1), ptr=4098), _Fake((4096, 4096), (4096, 1)))
     assert cfg["family"] == "fast"
     fam = ctypes.c_int()
     _lib.check(_lib.tile_config(4096, 4096, 4096, 4096, 1, 4096, 1, 4098, 0, -1, None, None, None, None, None,
                                 ctypes.byref(fam), None))
     assert fam.value == 1  # F16ACC_FAMILY_GENERIC
+    # where the table picks 128x128 or 64x64, unit-stride rows are read in
+    # place at any even address (a row-major b moves 64x64 to 128x128)
     cfg = tile_config(_Fake((64, 64), (64, 1), ptr=4098), _Fake((64, 64), (64, 1)))
-    assert cfg["family"] == "generic"
+    assert (cfg["family"], cfg["tile"]) == ("reg", "128x128")
+    cfg = tile_config(_Fake((64, 64), (64, 1), ptr=4098), _Fake((64, 64), (1, 64)))
+    assert (cfg["family"], cfg["tile"]) == ("reg", "64x64")
+    # forced tiles, operands as given: 64x64 with a row-major b and 256x256
+    # gather (mm packs first for a forced tile)
+    for b_strides, tile in (((64, 1), "64x64"), ((1, 64), "256x256")):
+        _lib.check(_lib.tile_config(64, 64, 64, 64, 1, *b_strides, 4098, 4096, _lib.TILES.index(tile), None, None,
+                                    None, None, None, ctypes.byref(fam), None))
+        assert fam.value == 1, tile
+        assert tile_config(_Fake((64, 64), (64, 1), ptr=4098), _Fake((64, 64), b_strides), tile)["family"] == "fast"
 
 
 def test_bad_inputs_raise_value_error():

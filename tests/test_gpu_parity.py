@@ -202,9 +202,14 @@ def _packed_case(a, b):
 
 
 @pytest.mark.parametrize("case", ["odd_k", "odd_k_wt", "row_major_odd_n", "offset_view", "strided"])
-def test_packed_operands_match_oracle(case):
-    """Operands the fast kernels cannot read directly are packed (zero-padded
-    K) and run on a fast tile; results match the oracle exactly as well."""
+def test_misaligned_operands_match_oracle(case):
+    """Operands the direct-to-LDS copies cannot read: unit-stride rows at any
+    even address are read in place by the register-staged loader where the
+    table picks 128x128 or 64x64; anything else (and every case on a forced
+    256x256) is packed first (zero-padded K) and runs on a fast tile.  Both
+    ways match the oracle."""
+    from f16acc_amd.kernel import mm_tile
+
     M, K, N = 257, 1001, 193
     if case == "odd_k":  # a [M, K] with K % 8 != 0, b row-major
         a, b = rnd((M, K), 30), rnd((K, N), 31)
@@ -227,19 +232,67 @@ def test_packed_operands_match_oracle(case):
         a, b = abig[:, ::2], bbig[:, 1::3]
         ga, gb = abig.cuda()[:, ::2], bbig.cuda()[:, 1::3]
     a2, b2, K2, fast = _packed_case(ga, gb)
-    assert fast and K2 % 8 == 0 and K2 - a.shape[1] < 8
-    # packed copies start every row on a 128-byte line
-    if a2.data_ptr() != ga.data_ptr():
+    cfg = tile_config(ga, gb)
+    if case == "strided":
+        assert fast and K2 % 8 == 0 and K2 - a.shape[1] < 8 and cfg["family"] == "fast"
+        # packed copies start every row on a 128-byte line
         assert a2.stride(0) % 64 == 0 and a2.data_ptr() % 128 == 0
-    if b2.data_ptr() != gb.data_ptr():
         assert b2.stride(1) % 64 == 0 and b2.data_ptr() % 128 == 0
-    cfg = tile_config(a2, b2)
+    else:
+        assert cfg["family"] == "reg" and cfg["tile"] in ("128x128", "64x64"), cfg
+        assert a2.data_ptr() == ga.data_ptr() and b2.data_ptr() == gb.data_ptr() and K2 == a.shape[1]
     for out_dtype in (torch.float32, torch.float16):
         c, flags = mm_flags(ga, gb, out_dtype)
         ref, rflags = oracle(a, b, out_dtype, cfg)
         assert torch.equal(flags.cpu(), rflags)
         assert rel(c.cpu(), ref) < TOL, (case, out_dtype)
         assert rel(c.cpu(), a.double() @ b.double()) < 2e-3
+        # the same operands packed and run on 256x256
+        c256 = mm_tile(ga, gb, "256x256", out_dtype)
+        assert rel(c256.cpu(), oracle(a, b, out_dtype, tile_config(ga, gb, "256x256"))[0]) < TOL
+
+
+@pytest.mark.parametrize("tile", ["128x128", "64x64"])
+@pytest.mark.parametrize("case", ["odd_k_wt", "odd_k_row_major", "offset_views", "odd_n_row_major"])
+def test_reg_loader_equals_packed_copies_bit_for_bit(tile, case):
+    """The register-staged loader fills the LDS stages exactly as the
+    direct-to-LDS copies fill them from packed, zero-padded operands, so the
+    same tile gives the same bits either way: chunked and FP32 modes, ragged
+    M, N and K (units cut at K and, for a row-major b, at N), overflow redo
+    included (one row block of a is large enough to overflow its chunks)."""
+    from f16acc_amd.kernel import _pack, mm_tile
+
+    M, N, K = 200, 136, 777
+    if case == "odd_n_row_major":
+        N, K = 131, 320
+    abig = rnd((M + 1, K + 3), 80)
+    abig[64:80] *= 10000.0  # chunk sums past 65504 in one row block
+    if case == "offset_views":
+        ga = abig.cuda()[1:, 3:]
+        bbig = rnd((N + 5, K + 1), 81)
+        gb = bbig.cuda()[5:, 1:].t()
+    else:
+        ga = abig.cuda()[:M, :K]
+        if case in ("odd_k_wt",):
+            gb = rnd((N, K), 82).cuda().t()
+        else:
+            gb = rnd((K, N), 83).cuda()
+    if tile == "64x64" and gb.stride(1) == 1 and gb.stride(0) != 1:
+        pytest.skip("64x64 reads a row-major b through the generic path")
+    cfg = tile_config(ga, gb, tile)
+    assert cfg["family"] == "reg", cfg
+    ld = -(-K // 64) * 64
+    pa = _pack(ga, M, K, ga.stride(0), ga.stride(1), ld)[:, :K + (-K % 8)]
+    pb = _pack(gb, N, K, gb.stride(1), gb.stride(0), ld)[:, :K + (-K % 8)].t()
+    assert tile_config(pa, pb, tile)["family"] == "fast"
+    for chunked in (True, False):
+        c_reg = mm_tile(ga, gb, tile, torch.float32, chunked=chunked)
+        c_fast = mm_tile(pa, pb, tile, torch.float32, chunked=chunked)
+        assert torch.equal(c_reg, c_fast), (tile, case, chunked)
+    _, flags = mm_flags(ga, gb, torch.float32, tile=tile)
+    ref, rflags = oracle(ga.cpu(), gb.cpu(), torch.float32, cfg)
+    assert torch.equal(flags.cpu(), rflags) and int(flags.sum()) > 0
+    assert rel(c_reg.cpu(), (ga.cpu().float() @ gb.cpu().float()).double()) < 1e-5
 
 
 def test_odd_config_2049_1537_8961():
@@ -248,12 +301,22 @@ def test_odd_config_2049_1537_8961():
     last, one-element chunk."""
     a, w = rnd((2049, 8961), 40), rnd((1537, 8961), 41, 0.02)
     ga, gw = a.cuda(), w.cuda()
+    from f16acc_amd.kernel import _pack, mm_tile
+
     c, flags = mm_flags(ga, gw.t(), torch.float32)
-    a2, b2, _, fast = _packed_case(ga, gw.t())
-    assert fast
-    ref, rflags = oracle(a, w.t(), torch.float32, tile_config(a2, b2))
+    cfg = tile_config(ga, gw.t())
+    assert (cfg["family"], cfg["tile"]) == ("fast", "128x128")  # packed: cheaper than in place at this size
+    ref, rflags = oracle(a, w.t(), torch.float32, cfg)
     assert int(flags.sum()) == 0 and int(rflags.sum()) == 0
     assert rel(c.cpu(), ref) < TOL
+    # forced, the tile reads the rows in place: the same bits as the same
+    # tile on packed copies, and the oracle's result
+    assert tile_config(ga, gw.t(), "128x128")["family"] == "reg"
+    c_reg = mm_tile(ga, gw.t(), "128x128", torch.float32)
+    pa = _pack(ga, 2049, 8961, 8961, 1, 9024)[:, :8968]
+    pw = _pack(gw, 1537, 8961, 8961, 1, 9024)[:, :8968]
+    assert torch.equal(c_reg, mm_tile(pa, pw.t(), "128x128", torch.float32))
+    assert rel(c_reg.cpu(), ref) < TOL
 
 
 def test_overflow_stress_flags_exactly_the_block_intersections():
