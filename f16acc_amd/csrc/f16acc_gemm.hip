@@ -37,8 +37,12 @@
 //   NC  (b N-contiguous, row-major [K, N]):
 //       k-row holds BN n as BN/8 units, unit u stored at u ^ nc_swz(k);
 //       fragments are ds_read_b64_tr_b16 (LDS transpose read).
-// Operands whose strides or alignment do not fit these paths go through a
-// generic kernel that gathers elements through registers into the KC layout.
+// Operands with unit-stride rows that are not 16-byte aligned (odd K,
+// offset views) can instead be loaded 16 bytes at a time at any even
+// address into registers and stored into the same layouts (RegLoader, on
+// the 128x128 and 64x64 tiles).  Operands whose strides fit neither path go
+// through a generic kernel that gathers elements through registers into the
+// KC layout.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
