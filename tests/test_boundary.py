@@ -220,3 +220,28 @@ def test_ragged_round_tail_plan(M, N, K, want):
     assert n.value == want
     assert _lib.tail_split(-1, N, K, K, 1, 1, K, 0, 0, ctypes.byref(n)) == -1  # F16ACC_E_ARG
 
+
+
+@pytest.mark.parametrize("M,N,K,in_place", [
+    (256, 256, 1001, True),      # a copy costs more than the GEMM
+    (2048, 1536, 1537, True),    # Qwen q/o with odd K: close, in place wins
+    (1024, 4096, 1001, True),
+    (2049, 1537, 8961, False),   # the odd config: the copy is cheaper than ~1.4x GEMM time
+    (2048, 1536, 8959, False),
+    (8192, 8192, 8191, False),
+])
+def test_in_place_reads_only_where_they_beat_a_copy(M, N, K, in_place):
+    """mm reads unit-stride misaligned rows in place (register-staged loads)
+    when that is cheaper than packing them: decided per shape from the
+    measured costs, then only where the library reports the 'reg' family."""
+    from f16acc_amd.kernel import _pack_plan, _reg_beats_pack
+
+    assert _reg_beats_pack(M, N, K) == in_place
+    a = _Fake((M, K), (K, 1))         # rows K halves long: misaligned for odd K
+    b = _Fake((K, N), (1, K))         # w.t() of an [N, K] weight
+    pack_a, pack_b, Kp, ld = _pack_plan(a, b, M, N, K)
+    fam = tile_config(a, b)["family"]
+    if in_place and fam == "reg":
+        assert (pack_a, pack_b, Kp) == (False, False, K)
+    else:
+        assert pack_a and pack_b and Kp % 8 == 0 and ld % 64 == 0 and fam == "fast"
