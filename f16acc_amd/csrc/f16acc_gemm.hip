@@ -216,30 +216,35 @@ __device__ __forceinline__ void wait_vm0() { wait_vm<0>(); }
 // ---------------------------------------------------------------------------
 template <class C>
 struct FastLoader {
-  int a_off[C::LA];   // byte offset inside the stage's rebased A window (or kOob)
-  int a_k[C::LA];     // first k of the unit (relative to the stage)
-  int b_off[C::LB];
-  int b_k[C::LB];     // KC: first k of the unit; NC: k-row of the unit
+  // Unit j of a thread sits j * RA rows (A, KC b) or j * RB k-rows (NC b)
+  // below its unit 0, at the same swizzled column (the swizzles repeat
+  // every 16 rows; RA and RB are multiples of 16), so a thread keeps unit 0
+  // only: byte offsets inside the stage's rebased windows, first k (KC) or
+  // k-row (NC), and how many rows below unit 0 stay inside M (N for a KC b).
+  static constexpr int RA = C::T / 8, RB = C::BL == kKC ? C::T / 8 : C::T / C::UB;
+  static_assert(RA % 16 == 0 && RB % 16 == 0, "unit rows must keep the swizzle phase");
+  int a_off, a_k, a_left;
+  int b_off, b_k, b_left;
+  int a_step, b_step;  // bytes between consecutive units (wave-uniform)
 
   __device__ __forceinline__ void init(const Params& p, int64_t m0, int64_t n0, int tid) {
-#pragma unroll
-    for (int j = 0; j < C::LA; ++j) {
-      const int s = j * C::T + tid, row = s >> 3, u = (s & 7) ^ kc_swz(row);
-      a_off[j] = (m0 + row < p.M) ? (int)(row * p.sam * 2 + u * 16) : kOob;
-      a_k[j] = 8 * u;
-    }
-#pragma unroll
-    for (int j = 0; j < C::LB; ++j) {
-      const int s = j * C::T + tid;
-      if (C::BL == kKC) {
-        const int row = s >> 3, u = (s & 7) ^ kc_swz(row);
-        b_off[j] = (n0 + row < p.N) ? (int)(row * p.sbn * 2 + u * 16) : kOob;
-        b_k[j] = 8 * u;
-      } else {
-        const int krow = s / C::UB, u = (s % C::UB) ^ (nc_swz(krow) & (C::UB - 1));
-        b_off[j] = (n0 + 8 * u < p.N) ? (int)(krow * p.sbk * 2 + u * 16) : kOob;
-        b_k[j] = krow;
-      }
+    const int row = tid >> 3, u = (tid & 7) ^ kc_swz(row);
+    a_off = (int)(row * p.sam * 2 + u * 16);
+    a_k = 8 * u;
+    a_left = (int)(p.M - m0 - row < C::BM ? p.M - m0 - row : C::BM);
+    a_step = __builtin_amdgcn_readfirstlane((int)(RA * p.sam * 2));
+    if (C::BL == kKC) {
+      const int brow = tid >> 3, bu = (tid & 7) ^ kc_swz(brow);
+      b_off = (int)(brow * p.sbn * 2 + bu * 16);
+      b_k = 8 * bu;
+      b_left = (int)(p.N - n0 - brow < C::BN ? p.N - n0 - brow : C::BN);
+      b_step = __builtin_amdgcn_readfirstlane((int)(RB * p.sbn * 2));
+    } else {
+      const int krow = tid / C::UB, bu = (tid % C::UB) ^ (nc_swz(krow) & (C::UB - 1));
+      b_off = (int)(krow * p.sbk * 2 + bu * 16);
+      b_k = krow;
+      b_left = n0 + 8 * bu < p.N ? kStageK : 0;  // the unit's columns inside N: every k-row, else none
+      b_step = __builtin_amdgcn_readfirstlane((int)(RB * p.sbk * 2));
     }
   }
 
@@ -250,11 +255,15 @@ struct FastLoader {
     int lds, krem;
     const FastLoader* ld;
     __device__ __forceinline__ void unit(int j) const {
-      if (j < C::LA)
-        lds_dma16(ra, lds + j * C::T * 16, ld->a_k[j] < krem ? ld->a_off[j] : kOob);
-      else
-        lds_dma16(rb, lds + C::A_STAGE + (j - C::LA) * C::T * 16,
-                  ld->b_k[j - C::LA] < krem ? ld->b_off[j - C::LA] : kOob);
+      if (j < C::LA) {
+        const bool ok = j * RA < ld->a_left && ld->a_k < krem;
+        lds_dma16(ra, lds + j * C::T * 16, ok ? ld->a_off + j * ld->a_step : kOob);
+      } else {
+        const int jb = j - C::LA;
+        const bool ok = C::BL == kKC ? jb * RB < ld->b_left && ld->b_k < krem
+                                     : ld->b_k + jb * RB < krem && jb * RB < ld->b_left;
+        lds_dma16(rb, lds + C::A_STAGE + jb * C::T * 16, ok ? ld->b_off + jb * ld->b_step : kOob);
+      }
     }
     __device__ __forceinline__ void all() const {
 #pragma unroll
