@@ -608,13 +608,44 @@ struct RegLoader {
     }
   }
 
+  // The same loads for a stage whose K range is whole (kend - kbase >= 64)
+  // in a tile whose row-major b units all lie inside N: every unit is then 8
+  // elements, so every load is issued unconditionally, a unit past M (or N
+  // for a K-contiguous b) at the tile's first row; store() zeroes those.  No
+  // load sits behind a branch or feeds an instruction before store(), so
+  // the loads of a stage stay in flight together.
+  __device__ __forceinline__ void load_full(const Params& p, int64_t m0, int64_t n0, int64_t kbase,
+                                            f16x8 (&buf)[C::LA + C::LB]) const {
+    const f16* wa = p.a + m0 * p.sam + kbase + a_k;
+#pragma unroll
+    for (int j = 0; j < C::LA; ++j) {
+      const int r = a_row + j * RA;
+      buf[j] = *(const f16x8_a2*)(wa + (int64_t)(m0 + r < p.M ? r : 0) * p.sam);
+    }
+#pragma unroll
+    for (int j = 0; j < C::LB; ++j) {
+      if (C::BL == kKC) {
+        const int r = b_row + j * RB;
+        buf[C::LA + j] = *(const f16x8_a2*)(p.b + n0 * p.sbn + kbase + b_k + (int64_t)(n0 + r < p.N ? r : 0) * p.sbn);
+      } else {
+        buf[C::LA + j] = *(const f16x8_a2*)(p.b + (kbase + b_row + (int64_t)j * RB) * p.sbk + n0 + b_k);
+      }
+    }
+  }
+
   // LDS stores of loaded units into the stage at `slot`: unit j of thread
-  // tid goes where FastLoader's copy of it lands.
-  static __device__ __forceinline__ void store(const f16x8 (&buf)[C::LA + C::LB], char LDS_AS* slot, int tid) {
+  // tid goes where FastLoader's copy of it lands; units past M (N for a
+  // K-contiguous b) store zeros.
+  __device__ __forceinline__ void store(const Params& p, int64_t m0, int64_t n0, const f16x8 (&buf)[C::LA + C::LB],
+                                        char LDS_AS* slot, int tid) const {
 #pragma unroll
-    for (int j = 0; j < C::LA; ++j) *(f16x8 LDS_AS*)(slot + (j * C::T + tid) * 16) = buf[j];
+    for (int j = 0; j < C::LA; ++j)
+      *(f16x8 LDS_AS*)(slot + (j * C::T + tid) * 16) = m0 + a_row + j * RA < p.M ? buf[j] : f16x8{};
 #pragma unroll
-    for (int j = 0; j < C::LB; ++j) *(f16x8 LDS_AS*)(slot + C::A_STAGE + (j * C::T + tid) * 16) = buf[C::LA + j];
+    for (int j = 0; j < C::LB; ++j) {
+      const bool ok = C::BL == kNC || n0 + b_row + j * RB < p.N;
+      *(f16x8 LDS_AS*)(slot + C::A_STAGE + (j * C::T + tid) * 16) = ok ? buf[C::LA + j] : f16x8{};
+    }
   }
 };
 
@@ -630,9 +661,19 @@ __device__ __forceinline__ void k_loop_reg(const Params& p, int64_t m0, int64_t 
   const int64_t nsteps = (kend - kbeg + kStageK - 1) / kStageK;
   if (nsteps <= 0) return;
   f16x8 buf[C::LA + C::LB];
-  rl.load(p, m0, n0, kbeg, kend, buf);
-  RegLoader<C>::store(buf, smem, tid);
-  if (nsteps > 1) rl.load(p, m0, n0, kbeg + kStageK, kend, buf);
+  // load_full's extra addresses fit the registers of the 128x128 tile with a
+  // K-contiguous b only (elsewhere they spill)
+  constexpr bool kFull = C::BL == kKC && C::WPE <= 2;
+  const bool n_inside = C::BL == kKC || n0 + C::BN <= p.N;
+  auto load = [&](int64_t kbase) {  // uniform choice between the two forms
+    if (kFull && n_inside && kend - kbase >= kStageK)
+      rl.load_full(p, m0, n0, kbase, buf);
+    else
+      rl.load(p, m0, n0, kbase, kend, buf);
+  };
+  load(kbeg);
+  rl.store(p, m0, n0, buf, smem, tid);
+  if (nsteps > 1) load(kbeg + kStageK);
   __syncthreads();
   Pipe<C> pp;
   const typename FastLoader<C>::Stage none{};
@@ -640,8 +681,8 @@ __device__ __forceinline__ void k_loop_reg(const Params& p, int64_t m0, int64_t 
     char LDS_AS* cur = smem + (s & 1) * C::STAGE;
     compute_stage<C, CHUNKED>(cur, wm, wn, lane, acc, none, false, pp);
     if (s + 1 < nsteps) {
-      RegLoader<C>::store(buf, smem + ((s + 1) & 1) * C::STAGE, tid);
-      if (s + 2 < nsteps) rl.load(p, m0, n0, kbeg + (s + 2) * kStageK, kend, buf);
+      rl.store(p, m0, n0, buf, smem + ((s + 1) & 1) * C::STAGE, tid);
+      if (s + 2 < nsteps) load(kbeg + (s + 2) * kStageK);
     }
     __syncthreads();
   }
