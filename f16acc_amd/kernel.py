@@ -79,7 +79,7 @@ def _workspace(a, b, M, N, K):
         nbytes = _ws_sizes[key] = n.value
     if nbytes == 0:
         return None
-    skey = (a.device.index, torch.cuda.current_stream(a.device).cuda_stream)
+    skey = (a.device.index, _stream(a.device))
     ws = _workspaces.get(skey)
     if ws is None or ws.numel() < nbytes:
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=a.device)
@@ -125,7 +125,7 @@ def _fast_b(b, K, N):
 def _pack(src, rows, cols, s_r, s_c, ld):
     """Zero-padded contiguous [rows, ld] copy of a strided fp16 matrix (f16acc_pack)."""
     dst = torch.empty(rows, ld, device=src.device, dtype=torch.float16)
-    stream = torch.cuda.current_stream(src.device).cuda_stream
+    stream = _stream(src.device)
     _lib.check(_lib.pack(src.data_ptr(), dst.data_ptr(), rows, cols, s_r, s_c, rows, ld, stream))
     return dst
 
@@ -252,12 +252,18 @@ def tile_config(a, b, tile=None):
             "tiles_n": tn.value, "family": _FAMILIES[fam.value], "threads": thr.value}
 
 
+def _stream(dev):
+    """hipStream_t of the current torch stream on dev, as an integer."""
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)  # ~0.2 us against ~2 us for the public path
+    return raw(dev.index) if raw is not None else torch.cuda.current_stream(dev).cuda_stream
+
+
 def _launch(a, b, c, flags, M, N, K, chunked, tile=-1, bias=None, ws=None):
     dev = a.device
     if torch.cuda.current_device() != dev.index:
         with torch.cuda.device(dev):
             return _launch(a, b, c, flags, M, N, K, chunked, tile, bias, ws)
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = _stream(dev)
     ptrs = (a.data_ptr(), b.data_ptr(), c.data_ptr(), flags.data_ptr() if flags is not None else None)
     args = (M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1),
             _OUT[c.dtype], int(bool(chunked)), stream)

@@ -524,6 +524,23 @@ def test_ragged_round_tail_split_fused_bias():
 
 
 
+def test_launch_stream_is_the_current_torch_stream():
+    """The launch goes on torch's current stream of the operands' device (the
+    raw query the Python layer uses agrees with the public one), also inside
+    a stream context."""
+    from f16acc_amd.kernel import _stream
+
+    dev = torch.device("cuda", 0)
+    assert _stream(dev) == torch.cuda.current_stream(dev).cuda_stream
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        assert _stream(dev) == s.cuda_stream == torch.cuda.current_stream(dev).cuda_stream
+        a, b = rnd((300, 520), 97).cuda(), rnd((520, 200), 98).cuda()
+        c = f16acc.mm(a, b)
+    s.synchronize()
+    assert rel(c.cpu(), chunk32.mm(a.cpu(), b.cpu(), torch.float16, tile=(128, 128))) < TOL
+
+
 def test_concurrent_calls_on_two_streams_from_two_threads():
     """mm keeps no shared state (the reference hands best_config to its redo
     launch through a global, README.md:48): two host threads calling it on
