@@ -1154,13 +1154,26 @@ inline int64_t split_count(int64_t tiles, int64_t slots, int64_t nsteps) {
 
 // est (optional) receives the estimated time of the pick, in the units of the
 // estimate that decided it.
+// Time of n 256x256 tiles in rounds of `cus`, in the units of kTileRate: a
+// last, partial round of f = r / cus of the CUs runs at 0.73 + 0.27 f^3 of
+// a full round's time (one tile per CU; measured on MI355X at K = 1536 and
+// 4096: 45.1 -> 62.5 us and 108.7 -> 148.2 us from 16 to 256 tiles, 126.7 us
+// at 192), since fewer busy CUs share the clock and the memory system.
+inline double rounds_256(int64_t n, int cus) {
+  const double full = 256.0 * 256.0 / kTileRate[F16ACC_TILE_256x256];
+  const int64_t r = n % cus;
+  const double f = (double)r / cus;
+  return (double)(n / cus) * full + (r ? full * (0.73 + 0.27 * f * f * f) : 0.0);
+}
+
 inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = nullptr) {
   int best = 0;
   double best_t = 0;
   for (int id = 0; id < 4; ++id) {
     const TileInfo& t = kTiles[id];
     const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
-    const double est = (double)cdiv(tiles, cus) * t.bm * t.bn / kTileRate[id];
+    const double est = id == F16ACC_TILE_256x256 ? rounds_256(tiles, cus)
+                                                 : (double)cdiv(tiles, cus) * t.bm * t.bn / kTileRate[id];
     if (id == 0 || est < best_t * 0.999) {
       best = id;
       best_t = est;
@@ -1229,6 +1242,8 @@ inline bool plan_tail(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak,
       choose_tile(M - main * t.bm, N, K, cus, &tail);
     else
       choose_tile(M, N - main * t.bn, K, cus, &tail);
+    // the main part as whole rounds (its tile count is at most whole rounds'):
+    // a cut pays off only where it beats the partial round it replaces
     const double mixed = (double)cdiv(across * main, cus) * t.bm * t.bn / kTileRate[F16ACC_TILE_256x256] + tail;
     if (mixed < best * 0.999 || (mixed <= best * 1.001 && across * main > best_fill)) {
       best = mixed;

@@ -107,6 +107,7 @@ class _Fake:
     (8192, 8192, 8192, (8192, 1), (8192, 1), "fast", "256x256"),
     (2048, 151936, 1536, (1536, 1), (1, 1536), "fast", "256x256"),  # lm_head
     (2048, 8960, 1536, (1536, 1), (1, 1536), "fast", "128x128"),   # 280 256-tiles: ragged 2nd wave
+    (1024, 11008, 4096, (4096, 1), (1, 4096), "fast", "256x256"),  # 172 256-tiles: one partial round beats 688 128-tiles
     (2048, 1536, 1536, (1536, 1), (1, 1536), "fast", "64x64"),     # 192 128-tiles for 512 slots, K short
     (2048, 256, 1536, (1536, 1), (1, 1536), "fast", "64x64"),      # Qwen k/v: 32 128-tiles
     (2048, 1536, 8960, (8960, 1), (1, 8960), "fast", "128x128"),   # 192 128-tiles, long K: split in two
@@ -211,6 +212,8 @@ def test_patch_enable_disable_and_cpu_fallback():
     (8960, 2048, 1536, -8192),  # tall: the row cut fills the first round, the column cut would not
     (8960, 4096, 1536, -8192),  # only the row cut gains
     (4096, 8960, 1536, 8192),   # only the column cut gains
+    (4096, 11008, 4096, 0),     # a 69%-full last round costs less than the cut (measured 404.8 against 419.5 us)
+    (4096, 18944, 3584, 0),
 ])
 def test_ragged_round_tail_plan(M, N, K, want):
     """Where f16acc_gemm cuts a ragged last 256x256 round into a second launch
