@@ -1123,7 +1123,7 @@ constexpr double kTileRate[4] = {1.00, 0.87, 0.87, 0.89};
 // The per-shape table: the fast tile with the smallest estimated time.
 // Ties keep the larger tile.
 //
-// Small grids: when the pick leaves workgroup slots empty, the 64x64 tile is
+// Small grids: when the pick leaves CUs without a workgroup, the 64x64 tile is
 // weighed against it by rounds of full-occupancy workgroups:
 //   estimated time = ceil(tiles / (CUs x per_cu)) x tile area x per_cu / rate
 // where the pick may also split K (plan_split; the split's own estimate
@@ -1181,7 +1181,11 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
   }
   const TileInfo& t = kTiles[best];
   const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn), slots = (int64_t)cus * t.per_cu;
-  if (tiles < slots) {
+  // Small grids: only when some CUs would get no workgroup at all.  With one
+  // workgroup of the pick on every CU, neither a K split (a finishing
+  // launch) nor 64x64 helps: 1024 x 4096 x 4096 on 256 tiles of 128x128
+  // ran 51.7 us unsplit, 54.3 us split in two and 57.2 us on 64x64.
+  if (tiles < cus) {
     const TileInfo& s = kTiles[F16ACC_TILE_64x64];
     const int64_t stiles = cdiv(M, s.bm) * cdiv(N, s.bn);
     double est_best = (double)t.bm * t.bn * t.per_cu / kTileRate[best];
@@ -1340,6 +1344,7 @@ inline SplitPlan plan_split(const Choice& ch, int64_t M, int64_t N, int64_t K, i
   if (ch.family == F16ACC_FAMILY_GENERIC || ch.tile == F16ACC_TILE_256x256 || ch.tile == F16ACC_TILE_64x64) return sp;
   const TileInfo& t = kTiles[ch.tile];
   const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
+  if (tiles >= cus) return sp;  // every CU has a workgroup already (choose_tile)
   const int64_t slots = (int64_t)cus * t.per_cu;
   const int64_t nsteps = cdiv(K, kStageK);
   const int64_t splits = split_count(tiles, slots, nsteps);

@@ -108,6 +108,8 @@ class _Fake:
     (2048, 151936, 1536, (1536, 1), (1, 1536), "fast", "256x256"),  # lm_head
     (2048, 8960, 1536, (1536, 1), (1, 1536), "fast", "128x128"),   # 280 256-tiles: ragged 2nd wave
     (1024, 11008, 4096, (4096, 1), (1, 4096), "fast", "256x256"),  # 172 256-tiles: one partial round beats 688 128-tiles
+    (2048, 2048, 1536, (1536, 1), (1, 1536), "fast", "128x128"),   # 256 128-tiles: one per CU, no 64x64 (22.8 vs 24.1 us)
+    (1024, 4096, 4096, (4096, 1), (1, 4096), "fast", "128x128"),   # one per CU: no K split either (51.4 vs 54.1 us)
     (2048, 1536, 1536, (1536, 1), (1, 1536), "fast", "64x64"),     # 192 128-tiles for 512 slots, K short
     (2048, 256, 1536, (1536, 1), (1, 1536), "fast", "64x64"),      # Qwen k/v: 32 128-tiles
     (2048, 1536, 8960, (8960, 1), (1, 8960), "fast", "128x128"),   # 192 128-tiles, long K: split in two
@@ -248,3 +250,13 @@ def test_in_place_reads_only_where_they_beat_a_copy(M, N, K, in_place):
         assert (pack_a, pack_b, Kp) == (False, False, K)
     else:
         assert pack_a and pack_b and Kp % 8 == 0 and ld % 64 == 0 and fam == "fast"
+
+
+def test_k_split_only_where_cus_would_idle():
+    """The split-K workspace is asked for only when the pick's tiles leave some
+    CUs without a workgroup (Qwen2.5 down: 192 tiles of 128x128 for 256 CUs),
+    not when every CU already has one (1024 x 4096 x 4096: 256 tiles)."""
+    n = ctypes.c_size_t()
+    for (M, N, K), split in (((2048, 1536, 8960), True), ((1024, 4096, 4096), False), ((2048, 256, 4096), True)):
+        _lib.check(_lib.workspace_size(M, N, K, K, 1, 1, K, 0, 0, ctypes.byref(n)))
+        assert (n.value > 0) == split, (M, N, K)
