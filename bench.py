@@ -18,7 +18,9 @@ redo.  Prints one JSON line:
   hipblaslt   torch.mm (hipBLASLt) on the same inputs and GPU
   max_rel_err_vs_fp64 / max_rel_err_vs_oracle  the reference's error metric
 Other workloads (--workload) are sweeps for the design record, not bench lines;
---workload shapes reports every configured shape against hipBLASLt.
+--workload shapes reports every configured shape against hipBLASLt;
+--workload table_check times the per-shape table against every forced tile on
+llama-2-7B, llama-3-8B and Qwen2.5-7B layer shapes.
 """
 
 import argparse
@@ -166,6 +168,50 @@ def sweep_tiles(names, rounds=5):
         print(json.dumps(row), flush=True)
         del a, b
         torch.cuda.empty_cache()
+
+
+# Transformer layer shapes the per-shape table was checked on (the Qwen2.5-1.5B
+# ones are WORKLOADS): (model, hidden size, k/v width, MLP width)
+LLM_MODELS = (("llama2-7b", 4096, 4096, 11008), ("llama3-8b", 4096, 1024, 14336), ("qwen2.5-7b", 3584, 512, 18944))
+
+
+def table_check(tokens=(256, 1024, 4096), rounds=3):
+    """The per-shape table against every forced tile on the layer GEMMs of
+    LLM_MODELS at several token counts (x [M, K] @ w.t(), w [N, K] ~ N(0, 0.02),
+    fp16 out, chunked): per-call times in settled bursts (median of interleaved
+    rounds), the table's pick
+    (split along K and ragged-round cuts included) next to each tile alone.
+    Prints one JSON line per shape and a summary line."""
+    import f16acc_amd
+    from f16acc_amd import _lib
+    from f16acc_amd.kernel import mm_tile, tile_config
+
+    tiles = [t for t in _lib.TILES if t != "generic"]
+    ratios = []
+    for model, d, kv, ffn in LLM_MODELS:
+        for M in tokens:
+            for layer, N, K in (("q/o", d, d), ("k/v", kv, d), ("gate/up", ffn, d), ("down", d, ffn)):
+                g = torch.Generator().manual_seed(0)
+                a = torch.randn(M, K, generator=g).half().cuda()
+                b = (torch.randn(N, K, generator=g) * 0.02).half().cuda().t()
+                ops = {"table": lambda: f16acc_amd.mm(a, b)}
+                ops.update({tile: (lambda x=tile: mm_tile(a, b, x)) for tile in tiles})
+                runs = {k: [] for k in ops}
+                for _ in range(rounds):  # interleaved, so clock drift falls on all alike
+                    for k, op in ops.items():
+                        runs[k].append(settled_time(op))
+                t = {k: statistics.median(v) for k, v in runs.items()}
+                best = min(tiles, key=lambda k: t[k])
+                ratios.append(t[best] / t["table"])
+                print(json.dumps({"model": model, "layer": layer, "M": M, "N": N, "K": K,
+                                  "pick": tile_config(a, b)["tile"], "table_us": round(t["table"] * 1e6, 1),
+                                  "best_forced": best, "best_forced_us": round(t[best] * 1e6, 1),
+                                  "best_forced_over_table": round(ratios[-1], 3),
+                                  **{k: round(v * 1e6, 1) for k, v in t.items() if k != "table"}}), flush=True)
+                del a, b
+    print(json.dumps({"shapes": len(ratios), "table_at_least_as_fast": sum(r >= 0.999 for r in ratios),
+                      "within_5pct_of_best_forced": sum(r >= 0.95 for r in ratios),
+                      "worst_best_forced_over_table": round(min(ratios), 3)}), flush=True)
 
 
 def settled_time(op, burst_ms=40.0):
@@ -420,7 +466,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="gemm4096",
-                    choices=sorted(WORKLOADS) + ["copy", "overflow", "qwen2_prefill", "shapes"])
+                    choices=sorted(WORKLOADS) + ["copy", "overflow", "qwen2_prefill", "shapes", "table_check"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and oracle comparison")
     ap.add_argument("--preheat", type=float, default=PREHEAT_S,
                     help="seconds of back-to-back calls before the warm-up steps (0 for counter runs)")
@@ -436,6 +482,8 @@ def main():
 
     if args.workload == "copy":
         return copy_reference(args.steps, args.warmup)
+    if args.workload == "table_check":
+        return table_check()
     if args.workload == "shapes":
         return shapes_report(list(WORKLOADS))
     if args.workload == "overflow":
