@@ -749,6 +749,14 @@ __device__ __forceinline__ float with_bias(float v, const f16* bias, int64_t col
   return OUT32 ? v + b : (float)(f16)v + b;
 }
 
+// Staging position of 16-byte unit u of a staged row: XOR-swizzled by row so
+// the 16 rows one 16-lane group writes fall on distinct bank groups.
+template <int U>
+__device__ __forceinline__ int stg_swz(int u, int row) {
+  static_assert((U & (U - 1)) == 0, "staged rows must hold a power of two of units");
+  return u ^ (row % U);
+}
+
 // fp16 output of a tile, staged through LDS so that every lane stores 16
 // contiguous bytes and a row leaves as whole cache lines: the MFMA layout
 // alone gives 8-byte stores covering 32 bytes of a row per instruction,
@@ -785,7 +793,7 @@ __device__ __forceinline__ void store_tile_staged(const Params& p, int64_t m0, i
       const f32x2 lo = {v[0], v[1]}, hi = {v[2], v[3]};
       const f16x2 hl = __builtin_convertvector(lo, f16x2), hh = __builtin_convertvector(hi, f16x2);
       const f16x4 o = {hl[0], hl[1], hh[0], hh[1]};
-      *(f16x4 LDS_AS*)(w + row * ROW + ((u ^ (row % U)) << 4) + (g & 1) * 8) = o;
+      *(f16x4 LDS_AS*)(w + row * ROW + (stg_swz<U>(u, row) << 4) + (g & 1) * 8) = o;
     }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
   __builtin_amdgcn_wave_barrier();
@@ -795,7 +803,7 @@ __device__ __forceinline__ void store_tile_staged(const Params& p, int64_t m0, i
 #pragma unroll
   for (int it = 0; it < C::WTM * U / 64; ++it) {
     const int idx = it * 64 + lane, row = idx / U, u = idx % U;
-    const f16x8 v = *(const f16x8 LDS_AS*)(w + row * ROW + ((u ^ (row % U)) << 4));
+    const f16x8 v = *(const f16x8 LDS_AS*)(w + row * ROW + (stg_swz<U>(u, row) << 4));
     if (whole) {
       *(f16x8*)(cbase + row * p.scm + 8 * u) = v;
     } else if (row < rows_in) {
@@ -806,6 +814,75 @@ __device__ __forceinline__ void store_tile_staged(const Params& p, int64_t m0, i
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           if (8 * u + e < cols_in) dst[e] = v[e];
+      }
+    }
+  }
+}
+
+// fp32 output staged the same way: each lane then stores a 16-byte unit of
+// 4 consecutive floats, a row of the staged sub-tile leaves as whole cache
+// lines (the MFMA layout alone writes 64 bytes of a row per instruction).
+// An fp32 sub-tile is twice the fp16 bytes: where all waves' sub-tiles do
+// not fit in SMEM bytes at once (256x256: 256 KiB) they go in P passes of
+// WTN / P columns, each wave through its own slice (its LDS reads of one
+// pass complete before it writes the next: a wave's LDS operations run in
+// order).  Rows of c at any 4-byte aligned address; the edge of c element by
+// element.
+typedef f32x4 __attribute__((aligned(4))) f32x4_a4;
+
+template <class C, int SMEM>
+__device__ __forceinline__ void store_tile_staged32(const Params& p, int64_t m0, int64_t n0, int wm, int wn,
+                                                    int lane, int wave, char LDS_AS* smem,
+                                                    const f32x4 (&acc)[C::FM][C::FN]) {
+  constexpr int NW = C::WAVES_M * C::WAVES_N;
+  constexpr int P = (NW * C::WTM * C::WTN * 4 + SMEM - 1) / SMEM;
+  static_assert(C::FN % P == 0, "passes must split the wave tile's column blocks evenly");
+  constexpr int PW = C::WTN / P;  // columns per pass
+  constexpr int U = PW / 4;       // 16-byte units per staged row
+  constexpr int ROW = PW * 4;
+  static_assert(NW * C::WTM * ROW <= SMEM, "a pass must fit the LDS");
+  char LDS_AS* w = smem + wave * (C::WTM * ROW);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int64_t col0 = n0 + wn * C::WTN;
+  float* cbase = (float*)p.c + (m0 + wm * C::WTM) * p.scm + col0;
+  const int64_t rows_in = p.M - (m0 + wm * C::WTM), cols_in = p.N - col0;
+  const bool whole = p.vec_store && rows_in >= C::WTM && cols_in >= C::WTN;
+#pragma unroll
+  for (int pass = 0; pass < P; ++pass) {
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+      for (int jj = 0; jj < C::FN / P; ++jj) {
+        const int j = pass * (C::FN / P) + jj;
+        const int row = 16 * i + r16, u = 4 * jj + g;
+        f32x4 v = acc[i][j];
+        if (p.bias) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t col = col0 + 16 * j + 4 * g + r;
+            if (col < p.N) v[r] = with_bias<true>(v[r], p.bias, col);
+          }
+        }
+        *(f32x4 LDS_AS*)(w + row * ROW + (stg_swz<U>(u, row) << 4)) = v;
+      }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int it = 0; it < C::WTM * U / 64; ++it) {
+      const int idx = it * 64 + lane, row = idx / U, u = idx % U;
+      const f32x4 v = *(const f32x4 LDS_AS*)(w + row * ROW + (stg_swz<U>(u, row) << 4));
+      const int c = pass * PW + 4 * u;  // column inside the wave's sub-tile
+      if (whole) {
+        *(f32x4*)(cbase + row * p.scm + c) = v;
+      } else if (row < rows_in) {
+        float* dst = cbase + row * p.scm + c;
+        if (c + 4 <= cols_in) {
+          *(f32x4_a4*)dst = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (c + e < cols_in) dst[e] = v[e];
+        }
       }
     }
   }
@@ -889,6 +966,8 @@ __device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, 
   }
   if (!OUT32 && C::BM * C::BN * 2 <= SMEM && p.scn == 1)
     store_tile_staged<C>(p, m0, n0, wm, wn, lane, wave, smem, acc);
+  else if (OUT32 && p.scn == 1 && ((uintptr_t)p.c & 3) == 0)
+    store_tile_staged32<C, SMEM>(p, m0, n0, wm, wn, lane, wave, smem, acc);
   else
     store_tile<C, OUT32>(p, m0, n0, wm, wn, lane, acc);
 }
