@@ -54,6 +54,29 @@ def test_square_1024_matches_oracle_and_fp64(out_dtype, b_transposed):
     assert rel(c, a.double() @ b.double()) < 2e-3
 
 
+@pytest.mark.parametrize("n", [4096, 8192])
+def test_full_size_square_gemms_match_oracle_and_fp64(n):
+    """The square workloads at their full sizes, n^3 with A, B ~ N(0, 1):
+    fp16 and fp32 output, B row-major and as the w.t() view, each against the
+    oracle's FP32 chunk sum (computed once: the layouts hold the same values)
+    and against FP64 within the reference's published 5.1e-4 at 4096^3
+    (README.md:29; 4.8e-4 measured in its tests/test_f16acc.py:39).  These
+    seeds give at most 4.8e-4 against the oracle (one fp16 ulp at the top of
+    the 8192^3 output, |c| up to 518) and 4.4e-4 against FP64; the oracle
+    takes ~2 s at 4096^3 and ~11 s at 8192^3 on 16 host threads."""
+    a, b = rnd((n, n), 50), rnd((n, n), 51)
+    s = chunk32.chunked_sum(a, b)
+    assert bool(torch.isfinite(s).all())
+    ref64 = a.cuda().double() @ b.cuda().double()
+    for b_t in (False, True):
+        for out_dtype in (torch.float16, torch.float32):
+            c, flags, cfg = run(a, b, out_dtype, b_transposed=b_t)
+            assert cfg["tile"] == "256x256" and int(flags.sum()) == 0, (n, b_t, out_dtype, cfg)
+            assert rel(c, s.to(out_dtype)) < TOL, (n, b_t, out_dtype)
+            assert rel(c.cuda(), ref64) < 5.1e-4, (n, b_t, out_dtype)
+            del c
+
+
 @pytest.mark.parametrize("shape", [(1000, 777, 1234), (300, 256, 200), (129, 72, 136), (64, 40, 8),
                                    (257, 1536, 256), (33, 33, 33), (1, 64, 1)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
@@ -319,17 +342,18 @@ def test_odd_config_2049_1537_8961():
     assert rel(c_reg.cpu(), ref) < TOL
 
 
-def test_overflow_stress_flags_exactly_the_block_intersections():
-    """The overflow stress workload at 1024^2 x 1024 with 2 of 8 row-blocks of
-    a and column-blocks of b set to U(200, 255): only the 4 intersection tiles
-    overflow; they are flagged like the oracle's, equal the unsplit
-    FP32-accumulate mode bit for bit (the redo runs all of K in one workgroup:
-    same tile, same summation order), and every other tile matches the
-    oracle."""
+@pytest.mark.parametrize("n, blocks", [(1024, 2), (4096, 7)])
+def test_overflow_stress_flags_exactly_the_block_intersections(n, blocks):
+    """The overflow stress workload, n^3 with `blocks` of the n / 128
+    row-blocks of a and column-blocks of b set to U(200, 255) (at 4096, 7 of
+    32: 4.8 % of the 128 x 128 tiles): only the intersection tiles overflow;
+    they are flagged like the oracle's, equal the unsplit FP32-accumulate
+    mode bit for bit (the redo runs all of K in one workgroup: same tile,
+    same summation order), and every other tile matches the oracle."""
     import bench
     from f16acc_amd.kernel import mm_tile
 
-    a, b, rows, cols = bench.overflow_inputs(n=1024, blocks=2)
+    a, b, rows, cols = bench.overflow_inputs(n=n, blocks=blocks)
     ga, gb = a.cuda(), b.cuda()
     cfg = tile_config(ga, gb)
     c, flags = mm_flags(ga, gb, torch.float32)
@@ -342,7 +366,7 @@ def test_overflow_stress_flags_exactly_the_block_intersections():
     sm, sn = max(1, 128 // bm), max(1, 128 // bn)
     want = {(r * 128 // bm + i, q * 128 // bn + j) for r in rows for q in cols for i in range(sm) for j in range(sn)}
     assert {tuple(t) for t in flags.nonzero().tolist()} == want
-    mask = flags.bool().repeat_interleave(bm, 0).repeat_interleave(bn, 1)[:1024, :1024]
+    mask = flags.bool().repeat_interleave(bm, 0).repeat_interleave(bn, 1)[:n, :n]
     assert torch.equal(c[mask], c32[mask])
     assert rel(c.cpu()[~mask.cpu()], ref[~mask.cpu()]) < TOL
 
