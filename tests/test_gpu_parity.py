@@ -77,6 +77,46 @@ def test_full_size_square_gemms_match_oracle_and_fp64(n):
             del c
 
 
+@pytest.mark.parametrize("layer, n_out, n_in, biased", [("q/o", 1536, 1536, True), ("k/v", 256, 1536, True),
+                                                        ("gate/up", 8960, 1536, False), ("down", 1536, 8960, False),
+                                                        ("lm_head", 151936, 1536, False)])
+def test_qwen_layer_shapes_match_oracle(layer, n_out, n_in, biased):
+    """Qwen2.5-1.5B's linear layers at 2048 tokens: x ~ N(0, 1), weight
+    N(0, 0.02) stored [out, in] and multiplied as w.t(), q/k/v with an
+    N(0, 0.02) bias.  mm matches the oracle with no tile flagged, through
+    whatever the shape plans (64x64 tiles, split-K for down, the ragged-round
+    second launch for gate/up); the fused bias equals the unfused
+    `y = mm(x, w.t()); y += b` (f16acc/patch.py:28-30) bit for bit, and the
+    patched nn.Linear returns those bits."""
+    M = 2048
+    x, w = rnd((M, n_in), 60), rnd((n_out, n_in), 61, 0.02)
+    gx, gw = x.cuda(), w.cuda()
+    c = f16acc.mm(gx, gw.t())
+    s = chunk32.chunked_sum(x, w.t())
+    assert bool(torch.isfinite(s).all())
+    assert rel(c.cpu(), s.half()) < TOL, layer
+    if not biased:
+        return
+    bias = rnd((n_out,), 62, 0.02).cuda()
+    fused = f16acc.kernel.mm_bias(gx, gw.t(), bias)
+    unfused = c.clone()
+    unfused += bias
+    assert torch.equal(fused, unfused), layer
+    lin = torch.nn.Linear(n_in, n_out, device="cuda", dtype=torch.float16)
+    with torch.no_grad():
+        lin.weight.copy_(gw)
+        lin.bias.copy_(bias)
+    f16acc.enable()
+    try:
+        before = f16acc.calls["chunked"]
+        with torch.inference_mode():
+            y = lin(gx)
+        assert f16acc.calls["chunked"] == before + 1
+    finally:
+        f16acc.disable()
+    assert torch.equal(y, fused), layer
+
+
 @pytest.mark.parametrize("shape", [(1000, 777, 1234), (300, 256, 200), (129, 72, 136), (64, 40, 8),
                                    (257, 1536, 256), (33, 33, 33), (1, 64, 1)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
