@@ -80,8 +80,12 @@ def preheat(op, seconds=None):
     MI355X's shader clock dips a few milliseconds into a load and takes
     ~15 ms to settle again (a 4096^3 GEMM: ~152 us per call, ~205 us in the
     dip): a window timed straight after a short warm-up measures that
-    transient, for this kernel and hipBLASLt alike."""
+    transient, for this kernel and hipBLASLt alike.  One call completes
+    before the clock starts: torch.mm's first call sets hipBLASLt up for
+    longer than the whole pre-heat."""
     seconds = PREHEAT_S if seconds is None else seconds
+    op()
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < seconds:
         for _ in range(8):
