@@ -588,6 +588,43 @@ def test_ragged_round_tail_split_fused_bias():
 
 
 
+@pytest.mark.parametrize("shape", [(300, 200, 517), (512, 384, 256), (1024, 1024, 1024)])
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+def test_c_abi_writes_any_output_strides(shape, out_dtype):
+    """f16acc_gemm writes c at any element strides (scm, scn): column-major,
+    rows padded to a pitch that breaks 16-byte alignment, every other
+    column.  The tile and its arithmetic depend on a and b only, so each
+    result equals the same call's contiguous output bit for bit, and every
+    element of the surrounding buffer that is not part of c keeps its
+    sentinel."""
+    from f16acc_amd import _lib
+
+    M, N, K = shape
+    a, w = rnd((M, K), 70).cuda(), rnd((N, K), 71).cuda()
+    b = w.t()
+    out = _lib.OUT_F32 if out_dtype == torch.float32 else _lib.OUT_F16
+    stream = torch.cuda.current_stream().cuda_stream
+    want = torch.empty(M, N, device="cuda", dtype=out_dtype)
+    _lib.check(_lib.gemm(a.data_ptr(), b.data_ptr(), want.data_ptr(), None, M, N, K, a.stride(0), a.stride(1),
+                         b.stride(0), b.stride(1), N, 1, out, 1, stream))
+    sentinel = -7.0
+    layouts = {"column-major": (N * M, 1, M, lambda buf: buf.view(N, M).t()),
+               "pitch N+3": (M * (N + 3), N + 3, 1, lambda buf: buf.view(M, N + 3)[:, :N]),
+               "every other column": (M * 2 * N, 2 * N, 2, lambda buf: buf.view(M, 2 * N)[:, ::2])}
+    for name, (numel, scm, scn, view) in layouts.items():
+        buf = torch.full((numel + 64,), sentinel, device="cuda", dtype=out_dtype)
+        body = buf[32:32 + numel]
+        _lib.check(_lib.gemm(a.data_ptr(), b.data_ptr(), body.data_ptr(), None, M, N, K, a.stride(0), a.stride(1),
+                             b.stride(0), b.stride(1), scm, scn, out, 1, stream))
+        torch.cuda.synchronize()
+        c = view(body)
+        assert torch.equal(c, want), (name, shape, out_dtype)
+        written = torch.zeros(numel, dtype=torch.bool, device="cuda")
+        view(written.view(-1)).fill_(True)
+        untouched = torch.cat([buf[:32], body[~written], buf[32 + numel:]])
+        assert bool((untouched == sentinel).all()), (name, shape, out_dtype)
+
+
 def test_launch_stream_is_the_current_torch_stream():
     """The launch goes on torch's current stream of the operands' device (the
     raw query the Python layer uses agrees with the public one), also inside
