@@ -27,8 +27,12 @@ _FAMILIES = ("fast", "generic", "reg")
 
 # Split-K workspace for the FP32 partials, one per (device, stream): kernels
 # on one stream run one after another, so consecutive calls on a stream can
-# share it.
+# share it.  A workspace that a larger one replaces is kept, not freed: a HIP
+# graph captured earlier holds its address and writes there on every replay,
+# so its memory must never go to another tensor.  Sizes grow at least 2x, so
+# few are kept.
 _workspaces = {}
+_retired = []
 _ws_sizes = {}  # problem key -> f16acc_workspace_size result
 _WS_MEMO_MAX = 4096
 
@@ -82,7 +86,10 @@ def _workspace(a, b, M, N, K):
     skey = (a.device.index, _stream(a.device))
     ws = _workspaces.get(skey)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=a.device)
+        if ws is not None:
+            _retired.append(ws)
+        grown = 2 * ws.numel() if ws is not None else 0
+        ws = torch.empty(max(nbytes, grown, 1 << 20), dtype=torch.uint8, device=a.device)
         _workspaces[skey] = ws
     return ws
 

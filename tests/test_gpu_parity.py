@@ -714,6 +714,38 @@ def test_hip_graph_capture_replays_match_eager():
             assert torch.equal(o, e)
 
 
+def test_graph_keeps_its_split_k_workspace_when_a_larger_one_replaces_it():
+    """A graph captured with a split-K mm writes its FP32 partials to the
+    stream's workspace on every replay.  A later eager call on that stream
+    that needs a larger workspace must not free the captured one: a tensor
+    allocated afterwards, of the old workspace's size, keeps its contents
+    across replays, and every replay still equals the eager result."""
+    from f16acc_amd import kernel
+
+    x1, w1 = rnd((2048, 4096), 110).cuda(), rnd((256, 4096), 111, 0.02).cuda()  # 8 MiB of partials
+    x2, w2 = rnd((1024, 16384), 112).cuda(), rnd((512, 16384), 113, 0.02).cuda()  # 32 MiB
+    eager1 = f16acc.mm(x1, w1.t())
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    key = (x1.device.index, side.cuda_stream)
+    with torch.cuda.stream(side):
+        f16acc.mm(x1, w1.t())  # the workspace exists before capture
+        captured = kernel._workspaces[key]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            out = f16acc.mm(x1, w1.t())
+        eager2 = f16acc.mm(x2, w2.t())
+        assert kernel._workspaces[key] is not captured and kernel._workspaces[key].numel() > captured.numel()
+        victim = torch.full((captured.numel(),), 0x5A, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager1)
+        assert bool((victim == 0x5A).all())
+    assert torch.equal(f16acc.mm(x2, w2.t()), eager2)
+
+
 def _random_operand(g, rows, cols, kind, seed):
     """A [rows, cols] fp16 CPU tensor laid out as `kind` (its GPU twin has the
     same strides): contiguous, transposed view, strided view or offset view."""
