@@ -20,7 +20,8 @@ redo.  Prints one JSON line:
 Other workloads (--workload) are sweeps for the design record, not bench lines;
 --workload shapes reports every configured shape against hipBLASLt;
 --workload table_check times the per-shape table against every forced tile on
-llama-2-7B, llama-3-8B and Qwen2.5-7B layer shapes.
+llama-2-7B, llama-3-8B and Qwen2.5-7B layer shapes; --tile-calls runs every tile
+untimed for rocprofv3 counter passes.
 """
 
 import argparse
@@ -170,6 +171,33 @@ def sweep_tiles(names, rounds=5):
         row = {"workload": name, "M": M, "N": N, "K": K, "b": layout, "table": tile_config(a, b)["tile"]}
         row.update({k: round(flops / statistics.median(v) / 1e12, 1) for k, v in times.items()})
         print(json.dumps(row), flush=True)
+        del a, b
+        torch.cuda.empty_cache()
+
+
+def tile_calls(names, calls):
+    """`calls` calls of every tile configuration the operands allow (forced),
+    of mm as shipped and of hipBLASLt on each workload, one after another with
+    a synchronisation between them and no timing: a run for rocprofv3 --pmc,
+    which reads each kernel's counters (MFMA busy cycles, LDS instructions,
+    HBM bytes) per dispatch."""
+    import f16acc_amd
+    from f16acc_amd import _lib
+    from f16acc_amd.kernel import mm_tile, tile_config
+
+    for name in names:
+        M, N, K, layout, out_dtype = WORKLOADS[name]
+        _, _, a, b = make_inputs(M, N, K, layout)
+        ops = {tile: (lambda t=tile: mm_tile(a, b, t, out_dtype)) for tile in _lib.TILES
+               if tile_config(a, b, tile)["tile"] == tile}
+        ops["mm"] = lambda: f16acc_amd.mm(a, b, out_dtype)
+        ops["hipblaslt"] = lambda: torch.mm(a, b)
+        for op in ops.values():
+            for _ in range(calls):
+                op()
+            torch.cuda.synchronize()
+        print(json.dumps({"workload": name, "M": M, "N": N, "K": K, "b": layout, "table": tile_config(a, b)["tile"],
+                          "ops": list(ops), "calls": calls}), flush=True)
         del a, b
         torch.cuda.empty_cache()
 
@@ -476,6 +504,9 @@ def main():
                     help="seconds of back-to-back calls before the warm-up steps (0 for counter runs)")
     ap.add_argument("--sweep-tiles", nargs="*", metavar="WORKLOAD",
                     help="time every tile configuration on these workloads (all if none given) and exit")
+    ap.add_argument("--tile-calls", nargs="+", metavar="WORKLOAD",
+                    help="run every tile configuration, mm and hipBLASLt --steps times each on these workloads, "
+                         "untimed (for rocprofv3 --pmc), and exit")
     args = ap.parse_args()
     PREHEAT_S = args.preheat
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -498,6 +529,8 @@ def main():
         return print(json.dumps(line), flush=True)
     if args.sweep_tiles is not None:
         return sweep_tiles(args.sweep_tiles or sorted(WORKLOADS))
+    if args.tile_calls:
+        return tile_calls(args.tile_calls, args.steps)
 
     import f16acc_amd
     from f16acc_amd.kernel import tile_config
