@@ -19,6 +19,8 @@ redo.  Prints one JSON line:
   max_rel_err_vs_fp64 / max_rel_err_vs_oracle  the reference's error metric
 Other workloads (--workload) are sweeps for the design record, not bench lines;
 --workload shapes reports every configured shape against hipBLASLt;
+--workload redo_overhead times the shipped kernels against a build without the
+overflow flag and redo on data that never overflows;
 --workload table_check times the per-shape table against every forced tile on
 llama-2-7B, llama-3-8B and Qwen2.5-7B layer shapes; --tile-calls runs every tile
 untimed for rocprofv3 counter passes.
@@ -123,12 +125,31 @@ def read_traffic():
         return None
 
 
+# Host threads the CPU baseline uses: a one-GPU job on the GPU box gets a
+# 16-core share of its host, whatever os.cpu_count() reports there.
+CPU_SHARE = 16
+
+
+def cpu_model():
+    """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            m = re.search(r"^model name\s*:\s*(.+)$", f.read(), re.M)
+        return m.group(1).strip() if m else None
+    except OSError:
+        return None
+
+
 def cpu_baseline(a, b, out_dtype, budget_s=20.0):
     """The reference algorithm (oracle.chunk32, PyTorch on the CPU) on this
-    host's cores, on the same inputs; repeated while within budget."""
+    host's cores: the full GEMM on the bench's own inputs, repeated (at most
+    3 runs) while within budget, plus the median of 5 at 1024^3 fp32 out
+    (the reference's CPU-runnable config).  Returns the baseline record and
+    the oracle's result for the bench inputs."""
     from oracle import chunk32
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    host = os.cpu_count() or 1
+    threads = max(1, min(CPU_SHARE, host))
     torch.set_num_threads(threads)
     M, K = a.shape
     N = b.shape[1]
@@ -139,9 +160,21 @@ def cpu_baseline(a, b, out_dtype, budget_s=20.0):
         ref = chunk32.mm(a, b, out_dtype)
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
+    g = torch.Generator().manual_seed(0)
+    a1, b1 = torch.randn(1024, 1024, generator=g).half(), torch.randn(1024, 1024, generator=g).half()
+    t1 = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        chunk32.mm(a1, b1, torch.float32)
+        t1.append(time.perf_counter() - t0)
+    t1 = statistics.median(t1)
     info = {"value": 2.0 * M * N * K / t / 1e12, "unit": "TFLOPS", "cores": threads, "kind": "port",
+            "host_cpus": host, "cpu_model": cpu_model(),
+            "thread_cap": f"{CPU_SHARE}: the GPU box's CPU share for one GPU",
             "sample": f"the full {M}x{N}x{K} GEMM (oracle/chunk32.py, torch CPU, {threads} threads), "
-                      f"median of {len(times)} run(s), {t:.2f} s each"}
+                      f"median of {len(times)} run(s), {t:.2f} s each",
+            "gemm1024_f32": {"value": round(2.0 * 1024 ** 3 / t1 / 1e12, 4), "unit": "TFLOPS",
+                             "ms": round(t1 * 1e3, 2), "runs": 5, "stat": "median"}}
     return info, ref
 
 
@@ -404,6 +437,69 @@ def overflow_bench(steps, warmup):
     print(json.dumps(line), flush=True)
 
 
+# Shapes of the redo-overhead A/B: the overflow stress config's no-overflow
+# twin (4096^3, A and B ~ N(0, 1), fp32 out), the 8192^3 square GEMM and the
+# Qwen2.5-1.5B layers at 2048 tokens (64x64 tiles, split-K with its finishing
+# launch, the ragged-round second launch).
+REDO_SHAPES = (("gemm4096_f32", 4096, 4096, 4096, "row", torch.float32),
+               ("gemm8192", 8192, 8192, 8192, "row", torch.float16),
+               ("qwen_qo", 2048, 1536, 1536, "t", torch.float16),
+               ("qwen_kv", 2048, 256, 1536, "t", torch.float16),
+               ("qwen_gateup", 2048, 8960, 1536, "t", torch.float16),
+               ("qwen_down", 2048, 1536, 8960, "t", torch.float16))
+
+
+def redo_overhead(rounds=7):
+    """What the overflow flag and the in-kernel FP32 redo cost when no tile
+    overflows: f16acc_gemm_ws (the entry mm uses: split-K where the table
+    splits) of the shipped library against the same source built with both
+    compiled out (libf16acc_amd_noredo.so, -DF16ACC_NO_REDO=1, loaded here
+    only), called through the C ABI on the same inputs, timed in interleaved
+    settled bursts (median over rounds).  Both must return the same bits on
+    this data (no tile overflows).  The reference calls an in-kernel redo 8 %
+    slower and a separate one "nearly free" (f16acc/kernel.py:6-9,
+    README.md:20)."""
+    import ctypes
+
+    from f16acc_amd import _lib, build
+
+    noredo = ctypes.CDLL(build.LIB_NOREDO)
+    gemm_noredo = noredo.f16acc_gemm_ws
+    gemm_noredo.argtypes, gemm_noredo.restype = _lib.gemm_ws.argtypes, _lib.gemm_ws.restype
+    ws = torch.empty(32 << 20, dtype=torch.uint8, device="cuda")  # every split on 256 CUs fits
+    for name, M, N, K, layout, out_dtype in REDO_SHAPES:
+        _, _, a, b = make_inputs(M, N, K, layout)
+        outs = {k: torch.empty(M, N, device="cuda", dtype=out_dtype) for k in ("shipped", "no_redo")}
+        stream = torch.cuda.current_stream().cuda_stream
+        code = _lib.OUT_F32 if out_dtype == torch.float32 else _lib.OUT_F16
+
+        def call(fn, c):
+            return lambda: _lib.check(fn(a.data_ptr(), b.data_ptr(), None, c.data_ptr(), None, M, N, K, a.stride(0),
+                                         a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1), code, 1,
+                                         stream, ws.data_ptr(), ws.numel()))
+
+        ops = {"shipped": call(_lib.gemm_ws, outs["shipped"]), "no_redo": call(gemm_noredo, outs["no_redo"])}
+        for op in ops.values():
+            op()
+        torch.cuda.synchronize()
+        same = bool(torch.equal(outs["shipped"], outs["no_redo"]))
+        times = {k: [] for k in ops}
+        for _ in range(rounds):
+            for k, op in ops.items():
+                times[k].append(settled_time(op))
+        t = {k: statistics.median(v) for k, v in times.items()}
+        print(json.dumps({"workload": name, "M": M, "N": N, "K": K,
+                          "b": "row-major [K,N]" if layout == "row" else "w.t()",
+                          "out": "fp32" if out_dtype == torch.float32 else "fp16",
+                          "us_shipped": round(t["shipped"] * 1e6, 2), "us_no_redo": round(t["no_redo"] * 1e6, 2),
+                          "redo_overhead_pct": round((t["shipped"] / t["no_redo"] - 1) * 100, 2),
+                          "per_round_pct": [round((x / y - 1) * 100, 2) for x, y in zip(times["shipped"],
+                                                                                        times["no_redo"])],
+                          "same_bits": same, "rounds": rounds}), flush=True)
+        del a, b, outs
+        torch.cuda.empty_cache()
+
+
 def qwen2_model(layers=28, seed=0, dtype=torch.float16):
     """Random-init Qwen2.5-1.5B architecture on the GPU: hidden 1536, SwiGLU
     8960, 12 query / 2 KV heads (head_dim 128), RMSNorm eps 1e-6, RoPE theta
@@ -498,7 +594,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="gemm4096",
-                    choices=sorted(WORKLOADS) + ["copy", "overflow", "qwen2_prefill", "shapes", "table_check"])
+                    choices=sorted(WORKLOADS) + ["copy", "overflow", "qwen2_prefill", "redo_overhead", "shapes",
+                                                 "table_check"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and oracle comparison")
     ap.add_argument("--preheat", type=float, default=PREHEAT_S,
                     help="seconds of back-to-back calls before the warm-up steps (0 for counter runs)")
@@ -523,6 +620,8 @@ def main():
         return shapes_report(list(WORKLOADS))
     if args.workload == "overflow":
         return overflow_bench(args.steps, args.warmup)
+    if args.workload == "redo_overhead":
+        return redo_overhead()
     if args.workload == "qwen2_prefill":
         line = {"workload": "random-init Qwen2.5-1.5B FP16 prefill, batch 1, 2048 seeded tokens",
                 **qwen2_prefill_ab()}

@@ -38,6 +38,10 @@ gemm_tile = _dll.f16acc_gemm_tile
 gemm_tile.argtypes = [_vp, _vp, _vp, _vp] + [_i64] * 9 + [_int, _int, _vp, _int]
 gemm_tile.restype = _int
 
+gemm_tile_ws = _dll.f16acc_gemm_tile_ws
+gemm_tile_ws.argtypes = [_vp, _vp, _vp, _vp] + [_i64] * 9 + [_int, _int, _vp, _int, _vp, ctypes.c_size_t]
+gemm_tile_ws.restype = _int
+
 pack = _dll.f16acc_pack
 pack.argtypes = [_vp, _vp] + [_i64] * 6 + [_vp]
 pack.restype = _int
@@ -63,9 +67,9 @@ abi_version.argtypes = []
 abi_version.restype = _int
 
 # Exported symbol names, as declared in include/f16acc.h.
-EXPORTS = ("f16acc_gemm", "f16acc_gemm_bias", "f16acc_gemm_ws", "f16acc_workspace_size", "f16acc_gemm_tile", "f16acc_pack", "f16acc_tile_config", "f16acc_block_tile", "f16acc_strerror",
+EXPORTS = ("f16acc_gemm", "f16acc_gemm_bias", "f16acc_gemm_ws", "f16acc_workspace_size", "f16acc_gemm_tile", "f16acc_gemm_tile_ws", "f16acc_pack", "f16acc_tile_config", "f16acc_block_tile", "f16acc_strerror",
            "f16acc_abi_version", "f16acc_tail_split")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OUT_F16, OUT_F32 = 0, 1
 E_ARG, E_UNSUPPORTED = -1, -2

@@ -19,6 +19,9 @@ CHUNKRATE_SRC = os.path.join(PKG, "csrc", "chunkrate.hip")
 INCLUDE = os.path.join(ROOT, "include")
 OUT_DIR = os.path.join(PKG, "_build")
 LIB = os.path.join(OUT_DIR, "libf16acc_amd.so")
+# The same source with the tile flag and FP32 redo compiled out
+# (-DF16ACC_NO_REDO=1): only bench.py's redo-overhead A/B loads it.
+LIB_NOREDO = os.path.join(OUT_DIR, "libf16acc_amd_noredo.so")
 CHUNKRATE = os.path.join(OUT_DIR, "chunkrate")  # MFMA / chunk-epilogue microbenchmark
 ARCH = "gfx950"
 
@@ -38,19 +41,25 @@ def hipcc():
     raise FileNotFoundError("hipcc not found (set HIPCC or install ROCm under /opt/rocm)")
 
 
-def _compile(flags, src, out, verbose):
-    """hipcc src -> out; the previous output is replaced atomically."""
+def _start(flags, src, out):
+    """Start hipcc src -> a temporary file next to out."""
     os.makedirs(OUT_DIR, exist_ok=True)
     fd, tmp = tempfile.mkstemp(suffix=".tmp", dir=OUT_DIR)
     os.close(fd)
     cmd = [hipcc(), *flags, "-I", INCLUDE, src, "-o", tmp]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
+    return cmd, tmp, out, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+
+
+def _finish(job, verbose):
+    """Wait for a hipcc job; the previous output is replaced atomically."""
+    cmd, tmp, out, proc = job
+    text, _ = proc.communicate()
+    if proc.returncode != 0:
         os.unlink(tmp)
-        raise RuntimeError("hipcc failed:\n" + " ".join(cmd) + "\n" + res.stdout + res.stderr)
+        raise RuntimeError("hipcc failed:\n" + " ".join(cmd) + "\n" + text)
     if verbose:
         noise = ("packed-fp32-ops", "warning generated", "warnings generated")
-        msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if not any(n in ln for n in noise)]
+        msgs = [ln for ln in text.splitlines() if not any(n in ln for n in noise)]
         if msgs:
             print("\n".join(msgs), file=sys.stderr)
     os.chmod(tmp, 0o755)
@@ -59,9 +68,19 @@ def _compile(flags, src, out, verbose):
 
 
 def build(verbose=False):
-    """Compile the library and the chunkrate microbenchmark."""
-    _compile(COMMON_FLAGS, CHUNKRATE_SRC, CHUNKRATE, verbose)
-    return _compile(HIP_FLAGS, SRC, LIB, verbose)
+    """Compile the library, its no-redo twin and the chunkrate
+    microbenchmark (three hipcc processes at once)."""
+    jobs = [_start(HIP_FLAGS, SRC, LIB), _start(HIP_FLAGS + ["-DF16ACC_NO_REDO=1"], SRC, LIB_NOREDO),
+            _start(COMMON_FLAGS, CHUNKRATE_SRC, CHUNKRATE)]
+    errors = []
+    for job in jobs:
+        try:
+            _finish(job, verbose)
+        except RuntimeError as e:
+            errors.append(str(e))
+    if errors:
+        raise RuntimeError("\n".join(errors))
+    return LIB
 
 
 if __name__ == "__main__":

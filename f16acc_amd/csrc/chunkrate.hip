@@ -12,6 +12,9 @@
 // shader-clock cycles (s_memtime) per "block step" per SIMD: two chunk MFMAs
 // of one 16x16 output block (ideal 32 cycles) plus whatever the variant adds.
 //
+//   part 0  numerics self-check of the two summation forms (pair selector
+//           MFMA, sparse quad selector v_smfmac) against a scalar host sum
+//           of the same FP16-rounded chunk partials; exits 1 on a mismatch
 //   part 1  which VALU instruction classes overlap an MFMA: per step one MFMA
 //           then four VALU ops of one class (16 cycles if fully hidden)
 //   part 2  complete chunk epilogues, software pipelined (the epilogue of
@@ -21,6 +24,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <vector>
@@ -240,6 +244,129 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   if (threadIdx.x == 0) cyc[blockIdx.x] = t1 - t0;
 }
 
+// ---- part 0: numerics self-check ----------------------------------------------
+// One wave: four chunk MFMAs (zero accumulator) of per-lane fragments a[c],
+// b[c]; the pair selector adds the FP16-rounded partials of chunks 0 and 1
+// to s_in, the sparse quad selector those of all four chunks: the same
+// instructions, operands and selector matrices as the timed loops above
+// (written with builtins here, so the compiler places the wait states
+// between an MFMA and the instructions reading its result).  Written out:
+// the FP32 partials and both sums, so the host can check them register by
+// register: whatever element a lane's register r holds, the selector must
+// leave
+//   s_in[r] + f16(P0[r]) + f16(P1[r])      (pair)
+//   s_in[r] + f16(P0[r]) + ... + f16(P3[r]) (quad)
+// in that same register.
+__global__ __launch_bounds__(64) void selfcheck_kernel(const f16x8* in_a, const f16x8* in_b, const f32x4* s_in,
+                                                       f32x4* p_out, f32x4* s_pair, f32x4* s_quad) {
+  typedef f16 f16x16 __attribute__((ext_vector_type(16)));
+  typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  const int lane = threadIdx.x;
+  f16x8 sel;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sel[e] = (4 * (lane >> 4) + (e >> 1) == (lane & 15)) ? (f16)1.0f : (f16)0.0f;
+  f16x8 sel4;
+  int idx;
+  quad_selector(lane, sel4, idx);
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 p[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    p[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(in_b[c * 64 + lane], in_a[c * 64 + lane], zero, 0, 0, 0);
+    p_out[c * 64 + lane] = p[c];
+  }
+  f16x8 even, odd;  // v_cvt_pk_f16_f32 of (P0, P1) and (P2, P3), register r -> elements 2r, 2r+1
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const f16x2 e = __builtin_convertvector((f32x2){p[0][r], p[1][r]}, f16x2);
+    const f16x2 o = __builtin_convertvector((f32x2){p[2][r], p[3][r]}, f16x2);
+    even[2 * r] = e[0];
+    even[2 * r + 1] = e[1];
+    odd[2 * r] = o[0];
+    odd[2 * r + 1] = o[1];
+  }
+  s_pair[lane] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, even, s_in[lane], 0, 0, 0);
+  const f16x16 bb = __builtin_shufflevector(odd, even, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+  s_quad[lane] = __builtin_amdgcn_smfmac_f32_16x16x64_f16(sel4, bb, s_in[lane], idx, 0, 0);
+}
+
+// Host side of part 0.  Integer-valued inputs keep every partial and sum
+// exact in FP32 while the partials pass 2048, where binary16 rounds to even
+// integers: the sums must then match bit for bit.  Random N(0, 1) inputs
+// check the same within 2 ulp of the FP32 sum (the MFMA may round a
+// three- or five-term sum once where the host rounds it once too, in a
+// different association).  Returns the number of mismatches.
+int selfcheck(bool integers, unsigned seed, double* worst_ulp) {
+  std::vector<f16x8> ha(4 * 64), hb(4 * 64);
+  std::vector<f32x4> hs(64), hp(4 * 64), hpair(64), hquad(64);
+  unsigned st = seed;
+  auto rnd = [&]() {  // xorshift32
+    st ^= st << 13;
+    st ^= st >> 17;
+    st ^= st << 5;
+    return st;
+  };
+  auto gauss = [&]() {  // sum of 12 uniforms, minus 6: approximately N(0, 1)
+    double x = 0;
+    for (int i = 0; i < 12; ++i) x += (rnd() & 0xffffff) / 16777216.0;
+    return x - 6.0;
+  };
+  for (int i = 0; i < 4 * 64; ++i)
+    for (int e = 0; e < 8; ++e) {
+      // integer partials up to 32 * 15 * 31 = 14880, mostly past 2048
+      ha[i][e] = integers ? (f16)(float)(rnd() % 16) : (f16)(float)gauss();
+      hb[i][e] = integers ? (f16)(float)(rnd() % 32) : (f16)(float)gauss();
+    }
+  for (int i = 0; i < 64; ++i)
+    for (int r = 0; r < 4; ++r) hs[i][r] = integers ? (float)((int)(rnd() % 2001) - 1000) : (float)(100.0 * gauss());
+  f16x8 *da, *db;
+  f32x4 *ds, *dp, *dpair, *dquad;
+  CHECK(hipMalloc(&da, ha.size() * sizeof(f16x8)));
+  CHECK(hipMalloc(&db, hb.size() * sizeof(f16x8)));
+  CHECK(hipMalloc(&ds, hs.size() * sizeof(f32x4)));
+  CHECK(hipMalloc(&dp, hp.size() * sizeof(f32x4)));
+  CHECK(hipMalloc(&dpair, 64 * sizeof(f32x4)));
+  CHECK(hipMalloc(&dquad, 64 * sizeof(f32x4)));
+  CHECK(hipMemcpy(da, ha.data(), ha.size() * sizeof(f16x8), hipMemcpyHostToDevice));
+  CHECK(hipMemcpy(db, hb.data(), hb.size() * sizeof(f16x8), hipMemcpyHostToDevice));
+  CHECK(hipMemcpy(ds, hs.data(), hs.size() * sizeof(f32x4), hipMemcpyHostToDevice));
+  hipLaunchKernelGGL(selfcheck_kernel, dim3(1), dim3(64), 0, 0, da, db, ds, dp, dpair, dquad);
+  CHECK(hipGetLastError());
+  CHECK(hipDeviceSynchronize());
+  CHECK(hipMemcpy(hp.data(), dp, hp.size() * sizeof(f32x4), hipMemcpyDeviceToHost));
+  CHECK(hipMemcpy(hpair.data(), dpair, 64 * sizeof(f32x4), hipMemcpyDeviceToHost));
+  CHECK(hipMemcpy(hquad.data(), dquad, 64 * sizeof(f32x4), hipMemcpyDeviceToHost));
+  for (void* q : {(void*)da, (void*)db, (void*)ds, (void*)dp, (void*)dpair, (void*)dquad}) CHECK(hipFree(q));
+  int bad = 0, rounded = 0;
+  *worst_ulp = 0;
+  for (int l = 0; l < 64; ++l)
+    for (int r = 0; r < 4; ++r) {
+      double h[4];
+      for (int c = 0; c < 4; ++c) {
+        h[c] = (double)(float)(f16)hp[c * 64 + l][r];  // RNE to binary16, as v_cvt_pk_f16_f32
+        rounded += h[c] != (double)hp[c * 64 + l][r];
+      }
+      const double pair = (double)hs[l][r] + h[0] + h[1];
+      const double quad = pair + h[2] + h[3];
+      for (int which = 0; which < 2; ++which) {
+        const double want = which ? quad : pair;
+        const float got = which ? hquad[l][r] : hpair[l][r];
+        const double ulp = std::fmax(std::fabs(std::nextafter((float)want, INFINITY) - (float)want), 1e-30);
+        const double err = std::fabs((double)got - want) / ulp;
+        *worst_ulp = err > *worst_ulp ? err : *worst_ulp;
+        if (integers ? (double)got != want : err > 2.0) ++bad;
+      }
+    }
+  if (integers && rounded == 0) {
+    std::printf("self-check: no partial was rounded, the inputs do not exercise the rounding\n");
+    ++bad;
+  }
+  std::printf("self-check (%s inputs): %d of 512 sums off, %d of 1024 partials rounded to binary16, "
+              "worst %.2f ulp\n", integers ? "integer" : "N(0,1)", bad, rounded, *worst_ulp);
+  return bad;
+}
+
 struct Bufs {
   float* out = nullptr;
   unsigned long long* cyc = nullptr;
@@ -277,6 +404,14 @@ int main() {
   CHECK(hipGetDeviceProperties(&prop, 0));
   std::printf("chunkrate on %s (%s), %d CUs; cycles are shader clocks (s_memtime) per SIMD\n", prop.name,
               prop.gcnArchName, cus);
+  std::printf("part 0: pair selector MFMA and sparse quad selector vs a host sum of the rounded partials\n");
+  double ulp_int = 0, ulp_rand = 0;
+  const int bad = selfcheck(true, 12345u, &ulp_int) + selfcheck(false, 777u, &ulp_rand);
+  if (bad) {
+    std::printf("self-check FAILED\n");
+    return 1;
+  }
+  std::printf("self-check ok\n");
   for (int w = 1; w <= 2; ++w) {
     Bufs b;
     b.blocks = cus * w;  // 4 waves per workgroup: w waves per SIMD

@@ -71,6 +71,15 @@ constexpr int kNumXcd = 8;      // MI355X: workgroups are dealt round-robin over
 constexpr int kGroupM = 8;      // group-M swizzle width (reference G = 8, kernel.py:17)
 constexpr int kOob = 0x7fffff00;  // buffer offset past num_records: the load returns 0
 
+// F16ACC_NO_REDO=1 compiles the tile flag and the FP32 redo out of every
+// kernel.  Only the benchmark's redo-overhead measurement builds it, as a
+// separate library that the package never loads: its results are wrong
+// wherever a chunk overflows.
+#ifndef F16ACC_NO_REDO
+#define F16ACC_NO_REDO 0
+#endif
+constexpr bool kRedo = !F16ACC_NO_REDO;
+
 static_assert(kStageK == 2 * kChunk, "a stage holds exactly one chunk pair");
 
 struct Params {
@@ -948,14 +957,52 @@ __device__ __forceinline__ void store_tile(const Params& p, int64_t m0, int64_t 
   }
 }
 
+// Workgroup OR of the tile flag through one LDS word.  clear() runs at kernel
+// start, before any wave can reach set_and_read(), and its barrier orders
+// the clear before every set; set_and_read() has lane 0 of each wave whose
+// ballot holds a bad value store 1, and one barrier publishes the stores.
+// (One barrier at the tile's end where a general workgroup reduction costs
+// three and a dispatch-packet load.)
+struct TileFlag {
+  int LDS_AS* word;
+  __device__ __forceinline__ void clear(int tid) const {
+    if (tid == 0) *word = 0;
+    __syncthreads();
+  }
+  __device__ __forceinline__ int set_and_read(bool bad, int lane) const {
+    if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) *word = 1;
+    __syncthreads();
+    return *word;
+  }
+};
+
+// Store of a tile's FP32 sums: staged through LDS where the layout allows
+// (needs the LDS free: every wave's reads of the last K stage done).
+template <class C, bool OUT32, int SMEM>
+__device__ __forceinline__ void store_any(const Params& p, char LDS_AS* smem, int64_t m0, int64_t n0, int wave, int wm,
+                                          int wn, int lane, const f32x4 (&acc)[C::FM][C::FN]) {
+  if (!OUT32 && C::BM * C::BN * 2 <= SMEM && p.scn == 1)
+    store_tile_staged<C>(p, m0, n0, wm, wn, lane, wave, smem, acc);
+  else if (OUT32 && p.scn == 1 && ((uintptr_t)p.c & 3) == 0)
+    store_tile_staged32<C, SMEM>(p, m0, n0, wm, wn, lane, wave, smem, acc);
+  else
+    store_tile<C, OUT32>(p, m0, n0, wm, wn, lane, acc);
+}
+
 // Flag, redo and store of a finished FP32 tile sum (shared by the whole-K
-// kernel and the split-K finishing kernel).
+// kernel and the split-K finishing kernel).  The chunked sums are stored
+// first and the workgroup's flag is reduced while those stores drain, so a
+// tile that does not overflow waits on nothing extra; a flagged tile
+// (kernel.py:70-71) is then recomputed whole with FP32 accumulation
+// (kernel.py:75-81) and stored again over its first store.  Each thread
+// writes the same addresses in both stores (same layout), in program order,
+// so the redone values are the ones that remain.
 template <class C, int LD, bool CHUNKED, bool OUT32, int SMEM>
-__device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, FastLoader<C>& ld, const RegLoader<C>& rl, int* tile_bad,
-                                            int64_t tm, int64_t tn, int tid, int wave, int wm, int wn, int lane,
-                                            f32x4 (&acc)[C::FM][C::FN]) {
+__device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, FastLoader<C>& ld, const RegLoader<C>& rl,
+                                            const TileFlag& tf, int64_t tm, int64_t tn, int tid, int wave, int wm,
+                                            int wn, int lane, f32x4 (&acc)[C::FM][C::FN]) {
   const int64_t m0 = tm * C::BM, n0 = tn * C::BN;
-  if (CHUNKED) {
+  if (CHUNKED && kRedo) {
     // tile flag: any element of the FP32 sum inf or NaN (kernel.py:70-71)
     bool bad = false;
 #pragma unroll
@@ -964,30 +1011,25 @@ __device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, 
       for (int j = 0; j < C::FN; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) bad |= !(__builtin_fabsf(acc[i][j][r]) < __builtin_inff());
-    if (bad) *tile_bad = 1;
-    __syncthreads();
-    const int flag = *tile_bad;
+    store_any<C, OUT32, SMEM>(p, smem, m0, n0, wave, wm, wn, lane, acc);
+    // the flag's barrier also retires every wave's reads of its LDS staging
+    // slice before a redo's copies overwrite the LDS
+    const int flag = tf.set_and_read(bad, lane);
     if (p.flags && tid == 0) p.flags[tm * p.tiles_n + tn] = (uint8_t)flag;
-    if (flag) {
-      // redo the whole tile, all of K, with FP32 accumulation (kernel.py:75-81)
+    if (!flag) return;
+    // redo the whole tile, all of K, with FP32 accumulation (kernel.py:75-81)
 #pragma unroll
-      for (int i = 0; i < C::FM; ++i)
+    for (int i = 0; i < C::FM; ++i)
 #pragma unroll
-        for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (LD == kDma)
-        k_loop_fast<C, false>(p, m0, n0, 0, p.K, smem, ld, wave, wm, wn, lane, acc);
-      else if constexpr (LD == kReg)
-        k_loop_reg<C, false>(p, m0, n0, 0, p.K, smem, rl, tid, wm, wn, lane, acc);
-      else
-        k_loop_generic<C, false>(p, m0, n0, smem, tid, wm, wn, lane, acc);
-    }
+      for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (LD == kDma)
+      k_loop_fast<C, false>(p, m0, n0, 0, p.K, smem, ld, wave, wm, wn, lane, acc);
+    else if constexpr (LD == kReg)
+      k_loop_reg<C, false>(p, m0, n0, 0, p.K, smem, rl, tid, wm, wn, lane, acc);
+    else
+      k_loop_generic<C, false>(p, m0, n0, smem, tid, wm, wn, lane, acc);
   }
-  if (!OUT32 && C::BM * C::BN * 2 <= SMEM && p.scn == 1)
-    store_tile_staged<C>(p, m0, n0, wm, wn, lane, wave, smem, acc);
-  else if (OUT32 && p.scn == 1 && ((uintptr_t)p.c & 3) == 0)
-    store_tile_staged32<C, SMEM>(p, m0, n0, wm, wn, lane, wave, smem, acc);
-  else
-    store_tile<C, OUT32>(p, m0, n0, wm, wn, lane, acc);
+  store_any<C, OUT32, SMEM>(p, smem, m0, n0, wave, wm, wn, lane, acc);
 }
 
 // FP32 partials of a split tile, thread-private order: split s, block
@@ -1011,6 +1053,7 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) 
   __shared__ __attribute__((aligned(1024))) char smem_raw[kSmem];
   __shared__ int tile_bad;
   char LDS_AS* smem = (char LDS_AS*)smem_raw;
+  const TileFlag tf{(int LDS_AS*)&tile_bad};
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1026,8 +1069,7 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) 
   const int64_t m0 = tm * C::BM, n0 = tn * C::BN;
   const int64_t kbeg = nsplit > 1 ? split * p.kps : 0;
   const int64_t kend = nsplit > 1 && kbeg + p.kps < p.K ? kbeg + p.kps : p.K;
-
-  if (CHUNKED && tid == 0) tile_bad = 0;
+  if (CHUNKED && kRedo && p.mode != kPartial) tf.clear(tid);
 
   f32x4 acc[C::FM][C::FN];
 #pragma unroll
@@ -1061,7 +1103,7 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) 
                                                part_offset<C>(i, j, 0) * 4, 0);
     return;
   }
-  finish_tile<C, LD, CHUNKED, OUT32, kSmem>(p, smem, ld, rl, &tile_bad, tm, tn, tid, wave, wm, wn, lane, acc);
+  finish_tile<C, LD, CHUNKED, OUT32, kSmem>(p, smem, ld, rl, tf, tm, tn, tid, wave, wm, wn, lane, acc);
 }
 
 // Split-K finishing kernel (kFinish): one workgroup per tile adds the FP32
@@ -1075,13 +1117,14 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void 
   __shared__ __attribute__((aligned(1024))) char smem_raw[kSmem];
   __shared__ int tile_bad;
   char LDS_AS* smem = (char LDS_AS*)smem_raw;
+  const TileFlag tf{(int LDS_AS*)&tile_bad};
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
   const int64_t tile = xcd_order(blockIdx.x, p.tiles_m * p.tiles_n);
   int64_t tm, tn;
   group_m(tile, p.tiles_m, p.tiles_n, &tm, &tn);
-  if (CHUNKED && tid == 0) tile_bad = 0;
+  if (CHUNKED && kRedo) tf.clear(tid);
   const float* part = p.ws + tile * p.splits * (int64_t)(C::BM * C::BN);
   f32x4 acc[C::FM][C::FN];
 #pragma unroll
@@ -1097,7 +1140,7 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void 
   }
   FastLoader<C> unused;
   RegLoader<C> unused_rl;
-  finish_tile<C, kGather, CHUNKED, OUT32, kSmem>(p, smem, unused, unused_rl, &tile_bad, tm, tn, tid, wave, wm, wn, lane,
+  finish_tile<C, kGather, CHUNKED, OUT32, kSmem>(p, smem, unused, unused_rl, tf, tm, tn, tid, wave, wm, wn, lane,
                                                  acc);
 }
 
@@ -1538,7 +1581,7 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
 
 extern "C" {
 
-int f16acc_abi_version(void) { return 2; }
+int f16acc_abi_version(void) { return 3; }
 
 const char* f16acc_strerror(int code) {
   if (code == 0) return "success";
@@ -1639,6 +1682,14 @@ int f16acc_gemm_tile(const void* a, const void* b, void* c, uint8_t* tile_flags,
   if (tile < 0) return F16ACC_E_ARG;
   return gemm_impl(a, b, nullptr, c, tile_flags, M, N, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked, stream,
                    tile);
+}
+
+int f16acc_gemm_tile_ws(const void* a, const void* b, void* c, uint8_t* tile_flags, int64_t M, int64_t N, int64_t K,
+                        int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int out_dtype,
+                        int chunked, void* stream, int tile, void* workspace, size_t ws_bytes) {
+  if (tile < 0 || (workspace && ((uintptr_t)workspace % 256) != 0)) return F16ACC_E_ARG;
+  return gemm_impl(a, b, nullptr, c, tile_flags, M, N, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked, stream,
+                   tile, workspace, ws_bytes);
 }
 
 }  // extern "C"

@@ -150,6 +150,21 @@ int f16acc_gemm_tile(const void* a, const void* b, void* c, uint8_t* tile_flags,
                      int out_dtype, int chunked, void* stream, int tile);
 
 /*
+ * f16acc_gemm_tile with a split-K workspace, as f16acc_gemm_ws: a forced
+ * 256x128, 128x256 or 128x128 tile whose tiles leave CUs idle splits K the
+ * way the table's own 128x128 pick does (the 256x256 and 64x64 tiles never
+ * split).  A workspace of 32 MiB covers every split on a 256-CU GPU; a
+ * smaller one runs the problem unsplit.  For tuning, and for testing the
+ * split path on every tile that has one.
+ */
+int f16acc_gemm_tile_ws(const void* a, const void* b, void* c, uint8_t* tile_flags,
+                        int64_t M, int64_t N, int64_t K,
+                        int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                        int64_t scm, int64_t scn,
+                        int out_dtype, int chunked, void* stream, int tile,
+                        void* workspace, size_t ws_bytes);
+
+/*
  * Operand packing for the fast kernels: dst[r][c] = src[r*s_r + c*s_c] for
  * r < rows, c < cols, zero elsewhere in the rows_pad x ld destination
  * (contiguous, row stride ld; ld a multiple of 8, dst 16-byte aligned).

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(dll, name), name
     assert sorted(_lib.EXPORTS) == names
-    assert _lib.abi_version() == _lib.ABI_VERSION == 2
+    assert _lib.abi_version() == _lib.ABI_VERSION == 3
 
 
 def test_gemm_rejects_bad_arguments_before_launching():
@@ -57,6 +57,11 @@ def test_gemm_rejects_bad_arguments_before_launching():
     for bad_tile in (-1, len(_lib.TILES), 99):  # forced tile out of range
         assert _lib.gemm_tile(8, 8, 8, None, a["M"], a["N"], a["K"], a["sam"], a["sak"], a["sbk"], a["sbn"],
                               a["scm"], a["scn"], 0, 1, None, bad_tile) == _lib.E_ARG
+        assert _lib.gemm_tile_ws(8, 8, 8, None, a["M"], a["N"], a["K"], a["sam"], a["sak"], a["sbk"], a["sbn"],
+                                 a["scm"], a["scn"], 0, 1, None, bad_tile, None, 0) == _lib.E_ARG
+    # a workspace that is not 256-byte aligned
+    assert _lib.gemm_tile_ws(8, 8, 8, None, a["M"], a["N"], a["K"], a["sam"], a["sak"], a["sbk"], a["sbn"],
+                             a["scm"], a["scn"], 0, 1, None, 3, 8, 1 << 20) == _lib.E_ARG
 
 
 def test_block_to_tile_map_is_a_bijection():
