@@ -30,6 +30,10 @@ gemm_ws = _dll.f16acc_gemm_ws
 gemm_ws.argtypes = [_vp, _vp, _vp, _vp, _vp] + [_i64] * 9 + [_int, _int, _vp, _vp, ctypes.c_size_t]
 gemm_ws.restype = _int
 
+gemm_noalloc = _dll.f16acc_gemm_noalloc
+gemm_noalloc.argtypes = [_vp, _vp, _vp, _vp, _vp] + [_i64] * 9 + [_int, _int, _vp]
+gemm_noalloc.restype = _int
+
 workspace_size = _dll.f16acc_workspace_size
 workspace_size.argtypes = [_i64] * 7 + [_vp, _vp, ctypes.POINTER(ctypes.c_size_t)]
 workspace_size.restype = _int
@@ -67,12 +71,12 @@ abi_version.argtypes = []
 abi_version.restype = _int
 
 # Exported symbol names, as declared in include/f16acc.h.
-EXPORTS = ("f16acc_gemm", "f16acc_gemm_bias", "f16acc_gemm_ws", "f16acc_workspace_size", "f16acc_gemm_tile", "f16acc_gemm_tile_ws", "f16acc_pack", "f16acc_tile_config", "f16acc_block_tile", "f16acc_strerror",
+EXPORTS = ("f16acc_gemm", "f16acc_gemm_bias", "f16acc_gemm_ws", "f16acc_gemm_noalloc", "f16acc_workspace_size", "f16acc_gemm_tile", "f16acc_gemm_tile_ws", "f16acc_pack", "f16acc_tile_config", "f16acc_block_tile", "f16acc_strerror",
            "f16acc_abi_version", "f16acc_tail_split")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OUT_F16, OUT_F32 = 0, 1
-E_ARG, E_UNSUPPORTED = -1, -2
+E_ARG, E_UNSUPPORTED, E_SCRATCH, E_DEVICE = -1, -2, -3, -4
 TILES = ("256x256", "256x128", "128x256", "128x128", "generic", "64x64")  # F16ACC_TILE_* ids
 TILE_GENERIC = 4
 

@@ -1496,9 +1496,12 @@ inline SplitPlan plan_split(const Choice& ch, int64_t M, int64_t N, int64_t K, i
   return sp;
 }
 
+// strict_ws: a split the workspace cannot hold is an error (F16ACC_E_SCRATCH)
+// instead of an unsplit launch.
 int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* tile_flags, int64_t M, int64_t N,
               int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int out_dtype,
-              int chunked, void* stream, int forced_tile, void* workspace = nullptr, size_t ws_bytes = 0) {
+              int chunked, void* stream, int forced_tile, void* workspace = nullptr, size_t ws_bytes = 0,
+              bool strict_ws = false) {
   if (M < 0 || N < 0 || K < 0) return F16ACC_E_ARG;
   if (out_dtype != F16ACC_OUT_F16 && out_dtype != F16ACC_OUT_F32) return F16ACC_E_ARG;
   if (chunked != 0 && chunked != 1) return F16ACC_E_ARG;
@@ -1516,14 +1519,14 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
                                stream, F16ACC_TILE_256x256);
       if (rc != 0) return rc;
       return gemm_impl((const f16*)a + at * sam, b, bias, (char*)c + at * scm * esize, nullptr, M - at, N, K, sam,
-                       sak, sbk, sbn, scm, scn, out_dtype, chunked, stream, -1, workspace, ws_bytes);
+                       sak, sbk, sbn, scm, scn, out_dtype, chunked, stream, -1, workspace, ws_bytes, strict_ws);
     }
     const int rc = gemm_impl(a, b, bias, c, nullptr, M, at, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked,
                              stream, F16ACC_TILE_256x256);
     if (rc != 0) return rc;
     return gemm_impl(a, (const f16*)b + at * sbn, bias ? (const f16*)bias + at : nullptr,
                      (char*)c + at * scn * esize, nullptr, M, N - at, K, sam, sak, sbk, sbn, scm, scn, out_dtype,
-                     chunked, stream, -1, workspace, ws_bytes);
+                     chunked, stream, -1, workspace, ws_bytes, strict_ws);
   }
   const Choice ch = choose(M, N, K, sam, sak, sbk, sbn, a, b, forced_tile);
   Params p;
@@ -1544,6 +1547,7 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
   p.ws = nullptr;
   if (workspace) {
     const SplitPlan sp = plan_split(ch, M, N, K, cu_count());
+    if (strict_ws && sp.bytes > ws_bytes) return F16ACC_E_SCRATCH;
     if (sp.splits > 1 && ws_bytes >= sp.bytes) {
       p.mode = kPartial;
       p.splits = sp.splits;
@@ -1579,14 +1583,56 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Fixed split-K scratch for f16acc_gemm_noalloc: one array per GPU, held
+// from the library's first use on that GPU until the process ends.  A split
+// plan needs at most (workgroup slots) x (tile bytes in FP32): 512 x 64 KiB
+// for 128x128 and 256 x 128 KiB for 256x128 on a 256-CU MI355X, 32 MiB
+// either way.  Every split tile writes all of its partials before the
+// finishing launch reads them, so the array needs no clearing between calls.
+// Calls that overlap in time on one GPU share it and race.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+namespace {
+
+// Device address of `scratch` on the current device, looked up once per
+// device (hipGetSymbolAddress with that device current); the host-side name
+// `scratch` is not a device address and is never passed to a kernel.
+// Concurrent first calls on a device may both look it up; they store the
+// same address.
+int scratch_ptr(void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<void*> cached[kMaxDevices];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return F16ACC_E_UNSUPPORTED;
+  void* p = cached[dev].load(std::memory_order_acquire);
+  if (!p) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return F16ACC_E_UNSUPPORTED;
+    cached[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return 0;
+}
+
+}  // namespace
+
 extern "C" {
 
-int f16acc_abi_version(void) { return 3; }
+int f16acc_abi_version(void) { return 4; }
 
 const char* f16acc_strerror(int code) {
   if (code == 0) return "success";
   if (code == F16ACC_E_ARG) return "f16acc: invalid argument";
   if (code == F16ACC_E_UNSUPPORTED) return "f16acc: unsupported layout or extent";
+  if (code == F16ACC_E_SCRATCH)
+    return "f16acc: the split-K plan needs more than the 32 MiB fixed scratch of f16acc_gemm_noalloc";
+  if (code == F16ACC_E_DEVICE) return "f16acc: the stream belongs to another device than the current one";
   if (code > 0) return hipGetErrorString((hipError_t)code);
   return "f16acc: unknown error";
 }
@@ -1674,6 +1720,23 @@ int f16acc_gemm_ws(const void* a, const void* b, const void* bias, void* c, uint
   if (workspace && ((uintptr_t)workspace % 256) != 0) return F16ACC_E_ARG;
   return gemm_impl(a, b, bias, c, tile_flags, M, N, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked, stream, -1,
                    workspace, ws_bytes);
+}
+
+int f16acc_gemm_noalloc(const void* a, const void* b, const void* bias, void* c, uint8_t* tile_flags, int64_t M,
+                        int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int64_t scm,
+                        int64_t scn, int out_dtype, int chunked, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return F16ACC_E_ARG;
+  if (M == 0 || N == 0) return 0;
+  int dev = 0, sdev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+  if (e != hipSuccess) return (int)e;
+  if (sdev != dev) return F16ACC_E_DEVICE;
+  void* ws = nullptr;
+  const int rc = scratch_ptr(&ws);
+  if (rc != 0) return rc;
+  return gemm_impl(a, b, bias, c, tile_flags, M, N, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked, stream, -1,
+                   ws, kScratchBytes, true);
 }
 
 int f16acc_gemm_tile(const void* a, const void* b, void* c, uint8_t* tile_flags, int64_t M, int64_t N, int64_t K,

@@ -23,6 +23,8 @@ extern "C" {
 
 #define F16ACC_E_ARG (-1)        /* negative size, null pointer with work to do, bad enum */
 #define F16ACC_E_UNSUPPORTED (-2) /* a layout / extent this build cannot address */
+#define F16ACC_E_SCRATCH (-3)     /* f16acc_gemm_noalloc: split plan larger than its fixed scratch */
+#define F16ACC_E_DEVICE (-4)      /* f16acc_gemm_noalloc: stream on another device than the current one */
 
 /* Tile configurations of the per-shape table (f16acc_tile_config reports
  * which one a problem uses; f16acc_gemm_tile forces one). */
@@ -118,6 +120,30 @@ int f16acc_gemm_ws(const void* a, const void* b, const void* bias, void* c, uint
                    int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
                    int64_t scm, int64_t scn,
                    int out_dtype, int chunked, void* stream, void* workspace, size_t ws_bytes);
+
+/*
+ * f16acc_gemm_ws without a caller workspace and without any allocation: the
+ * split-K partials go to a fixed 32 MiB scratch array that the library
+ * holds in device memory on each GPU it runs on, from its first use there
+ * until the process ends.  No counterpart in the reference; it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments and results as
+ * f16acc_gemm_ws (bias may be NULL).
+ *
+ *   - The first call on a device looks up that device's scratch address
+ *     (hipGetSymbolAddress); the current device must be the stream's
+ *     (F16ACC_E_DEVICE otherwise).
+ *   - A split plan larger than the scratch returns F16ACC_E_SCRATCH before
+ *     any launch (on a 256-CU MI355X every plan fits: at most 32 MiB).
+ *   - Calls that overlap in time on one GPU share its scratch and race:
+ *     serialise them (one stream, or events).  The scratch keeps the last
+ *     call's partials and needs no clearing.
+ */
+int f16acc_gemm_noalloc(const void* a, const void* b, const void* bias, void* c, uint8_t* tile_flags,
+                        int64_t M, int64_t N, int64_t K,
+                        int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                        int64_t scm, int64_t scn,
+                        int out_dtype, int chunked, void* stream);
 
 /*
  * The tile configuration f16acc_gemm picks for a problem: replaces the

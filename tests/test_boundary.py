@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(dll, name), name
     assert sorted(_lib.EXPORTS) == names
-    assert _lib.abi_version() == _lib.ABI_VERSION == 3
+    assert _lib.abi_version() == _lib.ABI_VERSION == 4
 
 
 def test_gemm_rejects_bad_arguments_before_launching():
@@ -59,6 +59,13 @@ def test_gemm_rejects_bad_arguments_before_launching():
                               a["scm"], a["scn"], 0, 1, None, bad_tile) == _lib.E_ARG
         assert _lib.gemm_tile_ws(8, 8, 8, None, a["M"], a["N"], a["K"], a["sam"], a["sak"], a["sbk"], a["sbn"],
                                  a["scm"], a["scn"], 0, 1, None, bad_tile, None, 0) == _lib.E_ARG
+    # the allocation-free entry: bad sizes rejected, an empty output is a no-op
+    assert _lib.gemm_noalloc(8, 8, None, 8, None, -1, a["N"], a["K"], a["sam"], a["sak"], a["sbk"], a["sbn"],
+                             a["scm"], a["scn"], 0, 1, None) == _lib.E_ARG
+    assert _lib.gemm_noalloc(8, 8, None, 8, None, 0, a["N"], a["K"], a["sam"], a["sak"], a["sbk"], a["sbn"],
+                             a["scm"], a["scn"], 0, 1, None) == 0
+    for code in (_lib.E_SCRATCH, _lib.E_DEVICE):
+        assert _lib.strerror(code).decode().startswith("f16acc: ")
     # a workspace that is not 256-byte aligned
     assert _lib.gemm_tile_ws(8, 8, 8, None, a["M"], a["N"], a["K"], a["sam"], a["sak"], a["sbk"], a["sbn"],
                              a["scm"], a["scn"], 0, 1, None, 3, 8, 1 << 20) == _lib.E_ARG
