@@ -154,29 +154,46 @@ enum Loader { kGather = 0, kDma = 1, kReg = 2 };
 // WPE: waves per SIMD the kernel is compiled for (amdgpu_waves_per_eu): 2
 // caps a wave at 256 registers, 4 at 128 (the 64x64 tile runs four
 // workgroups of four waves per CU).
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int NS_, int BL_, int WPE_ = 2>
+//
+// KG: K groups.  With KG > 1 the workgroup's waves form KG groups of
+// WAVES_M x WAVES_N waves; every group covers the whole output tile over its
+// own contiguous range of whole stages (so every chunk stays whole), with its
+// own LDS ring, and the groups' FP32 sums are added through the LDS in group
+// order, ((S_0 + S_1) + S_2) + ..., before the flag and the store.  That is
+// a K split inside one workgroup: shapes with few tiles (Qwen2.5-1.5B k/v
+// and q/o at 2048 tokens) get more waves per tile and shorter K loops
+// without a second launch or a workspace.
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int NS_, int BL_, int WPE_ = 2, int KG_ = 1>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, NS = NS_, BL = BL_;
-  static constexpr int WPE = WPE_;
-  static constexpr int T = 64 * WAVES_M * WAVES_N;
+  static constexpr int WPE = WPE_, KG = KG_;
+  static constexpr int NWG = WAVES_M * WAVES_N;                 // waves per K group
+  static constexpr int TG = 64 * NWG;                            // threads per K group
+  static constexpr int T = TG * KG;                              // threads per workgroup
   static constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;  // wave tile
   static constexpr int FM = WTM / 16, FN = WTN / 16;            // 16x16 MFMA blocks per wave
   static constexpr int A_STAGE = BM * kStageK * 2;               // bytes
   static constexpr int B_STAGE = BN * kStageK * 2;
   static constexpr int STAGE = A_STAGE + B_STAGE;
-  static constexpr int LA = BM * 8 / T;                          // 16-byte units per thread per stage
-  static constexpr int LB = BN * 8 / T;
+  static constexpr int RING = NS * STAGE;                        // one K group's LDS ring
+  static constexpr int LA = BM * 8 / TG;                         // 16-byte units per thread per stage
+  static constexpr int LB = BN * 8 / TG;
   static constexpr int UB = BN / 8;                              // NC: units per k-row
   static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave tile must be whole 16x16 blocks");
-  static_assert(BM * 8 % T == 0 && BN * 8 % T == 0, "stage must split evenly over threads");
+  static_assert(BM * 8 % TG == 0 && BN * 8 % TG == 0, "stage must split evenly over a group's threads");
   // The NC swizzle spreads a k-row over 16 units; at BN = 64 (8 units) it
   // folds onto 8 (still a permutation, some transpose reads then conflict).
-  static_assert(BL == kKC || BN >= 64, "NC k-rows need at least 8 units");
-  static_assert(NS >= 2 && NS * STAGE <= 160 * 1024, "LDS ring must fit the 160 KiB of a CU");
+  // It needs a power of two of units per k-row.
+  static_assert(BL == kKC || (BN >= 64 && (UB & (UB - 1)) == 0), "NC k-rows need 2^n >= 8 units");
+  static_assert(NS >= 2 && KG * RING <= 160 * 1024, "LDS rings must fit the 160 KiB of a CU");
+  static_assert(KG >= 1 && T <= 1024, "at most 1024 threads per workgroup");
+  // the group reduction parks groups 1..KG-1's sums in the (free) rings
+  static_assert((KG - 1) * BM * BN * 4 <= KG * RING, "group sums must fit the LDS rings");
   // Split-K partial stores are compiled only into tiles of 64x64 per wave:
   // at 64x128 per wave the chunked kernel already uses ~240 of its 256
-  // registers, and the extra path would make it spill.
-  static constexpr bool SPLITTABLE = FM * FN <= 16;
+  // registers, and the extra path would make it spill.  K-group tiles split
+  // inside the workgroup instead.
+  static constexpr bool SPLITTABLE = FM * FN <= 16 && KG == 1;
   static_assert((NS - 2) * (LA + LB) <= 63, "outstanding loads must fit vmcnt");
 };
 
@@ -232,7 +249,7 @@ struct FastLoader {
   // every 16 rows; RA and RB are multiples of 16), so a thread keeps unit 0
   // only: byte offsets inside the stage's rebased windows, first k (KC) or
   // k-row (NC), and how many rows below unit 0 stay inside M (N for a KC b).
-  static constexpr int RA = C::T / 8, RB = C::BL == kKC ? C::T / 8 : C::T / C::UB;
+  static constexpr int RA = C::TG / 8, RB = C::BL == kKC ? C::TG / 8 : C::TG / C::UB;
   static_assert(RA % 16 == 0 && RB % 16 == 0, "unit rows must keep the swizzle phase");
   int a_off, a_k, a_left;
   int b_off, b_k, b_left;
@@ -268,12 +285,12 @@ struct FastLoader {
     __device__ __forceinline__ void unit(int j) const {
       if (j < C::LA) {
         const bool ok = j * RA < ld->a_left && ld->a_k < krem;
-        lds_dma16(ra, lds + j * C::T * 16, ok ? ld->a_off + j * ld->a_step : kOob);
+        lds_dma16(ra, lds + j * C::TG * 16, ok ? ld->a_off + j * ld->a_step : kOob);
       } else {
         const int jb = j - C::LA;
         const bool ok = C::BL == kKC ? jb * RB < ld->b_left && ld->b_k < krem
                                      : ld->b_k + jb * RB < krem && jb * RB < ld->b_left;
-        lds_dma16(rb, lds + C::A_STAGE + jb * C::T * 16, ok ? ld->b_off + jb * ld->b_step : kOob);
+        lds_dma16(rb, lds + C::A_STAGE + jb * C::TG * 16, ok ? ld->b_off + jb * ld->b_step : kOob);
       }
     }
     __device__ __forceinline__ void all() const {
@@ -539,31 +556,98 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
 // later stages' copies that may stay outstanding), the barrier makes every
 // wave's copies visible and retires all reads of the slot stage s+NS-1 will
 // overwrite, then that copy is issued and stage s is multiplied.
+//
+// `iters` (at least the stage count) is the number of barrier steps: the K
+// groups of a workgroup share its barriers, so a group with fewer stages
+// than another keeps stepping, without work, until the longest is done.
+// `wave` is the wave's index inside its K group, smem that group's ring.
 template <class C, bool CHUNKED>
 __device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t n0, int64_t kbeg, int64_t kend,
                                             char LDS_AS* smem, FastLoader<C>& ld, int wave, int wm, int wn, int lane,
-                                            f32x4 (&acc)[C::FM][C::FN]) {
-  const int64_t nsteps = (kend - kbeg + kStageK - 1) / kStageK;
-  if (nsteps <= 0) return;
+                                            f32x4 (&acc)[C::FM][C::FN], int64_t iters = 0) {
+  const int64_t nsteps = kend > kbeg ? (kend - kbeg + kStageK - 1) / kStageK : 0;
+  if (iters < nsteps) iters = nsteps;
+  if (iters <= 0) return;
 #pragma unroll
   for (int s0 = 0; s0 < C::NS - 1; ++s0)
     if (s0 < nsteps) ld.issue(p, m0, n0, kbeg + (int64_t)s0 * kStageK, kend, smem + s0 * C::STAGE, wave);
   int slot = 0;
   Pipe<C> pp;
-  for (int64_t s = 0; s < nsteps; ++s) {
+  for (int64_t s = 0; s < iters; ++s) {
     if (s + C::NS - 2 < nsteps)
       wait_vm<(C::NS - 2) * (C::LA + C::LB)>();
     else
       wait_vm0();
     __syncthreads();
-    const int64_t nxt = s + C::NS - 1;
-    const int nslot = slot == 0 ? C::NS - 1 : slot - 1;  // (s + NS - 1) % NS
-    const typename FastLoader<C>::Stage next = ld.stage(p, m0, n0, kbeg + nxt * kStageK, kend, smem + nslot * C::STAGE, wave);
-    compute_stage<C, CHUNKED>(smem + slot * C::STAGE, wm, wn, lane, acc, next, nxt < nsteps, pp);
+    if (C::KG == 1 || s < nsteps) {
+      const int64_t nxt = s + C::NS - 1;
+      const int nslot = slot == 0 ? C::NS - 1 : slot - 1;  // (s + NS - 1) % NS
+      const typename FastLoader<C>::Stage next =
+          ld.stage(p, m0, n0, kbeg + nxt * kStageK, kend, smem + nslot * C::STAGE, wave);
+      compute_stage<C, CHUNKED>(smem + slot * C::STAGE, wm, wn, lane, acc, next, nxt < nsteps, pp);
+    }
     slot = slot + 1 == C::NS ? 0 : slot + 1;
   }
   if (CHUNKED && nsteps > 0) pipe_drain<C>(pp, lane, acc);
   __syncthreads();  // LDS free for a redo pass
+}
+
+// K range of K group g: the workgroup's range [kbeg, kend) in whole stages,
+// ceil(stages / KG) per group, in group order (group KG-1 may get fewer or
+// none).  Returns the group's stage count bound (the shared iteration count).
+template <class C>
+__device__ __forceinline__ int64_t group_range(int64_t kbeg, int64_t kend, int g, int64_t* gbeg, int64_t* gend) {
+  const int64_t nsteps = kend > kbeg ? (kend - kbeg + kStageK - 1) / kStageK : 0;
+  const int64_t per = (nsteps + C::KG - 1) / C::KG;
+  int64_t b = kbeg + (int64_t)g * per * kStageK, e = b + per * kStageK;
+  if (b > kend) b = kend;
+  if (e > kend) e = kend;
+  *gbeg = b;
+  *gend = e;
+  return per;
+}
+
+// Sum of the K groups' FP32 tile sums into group 0, in group order
+// (((S_0 + S_1) + S_2) + ...: deterministic).  Groups 1..KG-1 park their
+// sums in the LDS (free: every K loop ends with a barrier), one 16-byte unit
+// per thread and block, consecutive threads on consecutive units.  Ends with
+// a barrier, so the LDS is free again for the store's staging.
+template <class C>
+__device__ __forceinline__ void group_reduce(char LDS_AS* smem, int g, int ltid, f32x4 (&acc)[C::FM][C::FN]) {
+  if constexpr (C::KG > 1) {
+    if (g > 0) {
+      char LDS_AS* mine = smem + (g - 1) * (C::BM * C::BN * 4);
+#pragma unroll
+      for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) *(f32x4 LDS_AS*)(mine + ((i * C::FN + j) * C::TG + ltid) * 16) = acc[i][j];
+    }
+    __syncthreads();
+    if (g == 0) {
+#pragma unroll
+      for (int h = 1; h < C::KG; ++h) {
+        const char LDS_AS* theirs = smem + (h - 1) * (C::BM * C::BN * 4);
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+          for (int j = 0; j < C::FN; ++j)
+            acc[i][j] += *(const f32x4 LDS_AS*)(theirs + ((i * C::FN + j) * C::TG + ltid) * 16);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// The fast path's K loop over [kbeg, kend) for this thread's K group, then
+// the group reduction: group 0 ends with the tile's sum.
+template <class C, bool CHUNKED>
+__device__ __forceinline__ void k_groups_fast(const Params& p, int64_t m0, int64_t n0, int64_t kbeg, int64_t kend,
+                                              char LDS_AS* smem, FastLoader<C>& ld, int g, int ltid, int lw, int wm,
+                                              int wn, int lane, f32x4 (&acc)[C::FM][C::FN]) {
+  int64_t gbeg = kbeg, gend = kend, iters = 0;
+  if (C::KG > 1) iters = group_range<C>(kbeg, kend, g, &gbeg, &gend);
+  k_loop_fast<C, CHUNKED>(p, m0, n0, gbeg, gend, smem + g * C::RING, ld, lw, wm, wn, lane, acc, iters);
+  group_reduce<C>(smem, g, ltid, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -583,7 +667,7 @@ struct RegLoader {
   // below its unit 0, at the same swizzled column: the swizzles repeat every
   // 16 rows and T / 8, T / UB are multiples of 16.  So a thread keeps only
   // its unit 0.
-  static constexpr int RA = C::T / 8, RB = C::BL == kKC ? C::T / 8 : C::T / C::UB;
+  static constexpr int RA = C::TG / 8, RB = C::BL == kKC ? C::TG / 8 : C::TG / C::UB;
   static_assert(RA % 16 == 0 && RB % 16 == 0, "unit rows must keep the swizzle phase");
   int a_row, a_k;  // unit 0 of A: tile row, first k in the stage
   int b_row, b_k;  // unit 0 of B: KC tile column and first k; NC k-row and first column
@@ -669,11 +753,11 @@ struct RegLoader {
                                         char LDS_AS* slot, int tid) const {
 #pragma unroll
     for (int j = 0; j < C::LA; ++j)
-      *(f16x8 LDS_AS*)(slot + (j * C::T + tid) * 16) = m0 + a_row + j * RA < p.M ? buf[j] : f16x8{};
+      *(f16x8 LDS_AS*)(slot + (j * C::TG + tid) * 16) = m0 + a_row + j * RA < p.M ? buf[j] : f16x8{};
 #pragma unroll
     for (int j = 0; j < C::LB; ++j) {
       const bool ok = C::BL == kNC || n0 + b_row + j * RB < p.N;
-      *(f16x8 LDS_AS*)(slot + C::A_STAGE + (j * C::T + tid) * 16) = ok ? buf[C::LA + j] : f16x8{};
+      *(f16x8 LDS_AS*)(slot + C::A_STAGE + (j * C::TG + tid) * 16) = ok ? buf[C::LA + j] : f16x8{};
     }
   }
 };
@@ -725,7 +809,7 @@ __device__ __forceinline__ void stage_generic(const Params& p, int64_t m0, int64
                                               char LDS_AS* stage, int tid) {
 #pragma unroll 2
   for (int j = 0; j < C::LA; ++j) {
-    const int s = j * C::T + tid, row = s >> 3, u = (s & 7) ^ kc_swz(row);
+    const int s = j * C::TG + tid, row = s >> 3, u = (s & 7) ^ kc_swz(row);
     const int64_t m = m0 + row;
     f16x8 v;
 #pragma unroll
@@ -737,7 +821,7 @@ __device__ __forceinline__ void stage_generic(const Params& p, int64_t m0, int64
   }
 #pragma unroll 2
   for (int j = 0; j < C::LB; ++j) {
-    const int s = j * C::T + tid, row = s >> 3, u = (s & 7) ^ kc_swz(row);
+    const int s = j * C::TG + tid, row = s >> 3, u = (s & 7) ^ kc_swz(row);
     const int64_t n = n0 + row;
     f16x8 v;
 #pragma unroll
@@ -777,11 +861,15 @@ __device__ __forceinline__ float with_bias(float v, const f16* bias, int64_t col
 }
 
 // Staging position of 16-byte unit u of a staged row: XOR-swizzled by row so
-// the 16 rows one 16-lane group writes fall on distinct bank groups.
+// the 16 rows one 16-lane group writes fall on distinct bank groups (rows of
+// a power of two of units), else rotated by the row (48-column wave tiles:
+// 6 or 12 units).
 template <int U>
 __device__ __forceinline__ int stg_swz(int u, int row) {
-  static_assert((U & (U - 1)) == 0, "staged rows must hold a power of two of units");
-  return u ^ (row % U);
+  if constexpr ((U & (U - 1)) == 0)
+    return u ^ (row % U);
+  else
+    return (u + row) % U;
 }
 
 // fp16 output of a tile, staged through LDS so that every lane stores 16
@@ -997,21 +1085,29 @@ __device__ __forceinline__ void store_any(const Params& p, char LDS_AS* smem, in
 // (kernel.py:75-81) and stored again over its first store.  Each thread
 // writes the same addresses in both stores (same layout), in program order,
 // so the redone values are the ones that remain.
+//
+// K-group tiles (C::KG > 1): acc holds the tile's sum in group 0 only
+// (group_reduce), so group 0 flags and stores; every group takes part in the
+// barriers, and a redo runs as the main pass did, each group over its own K
+// range (in FP32), then the same reduction.  g is the thread's K group, lw
+// its wave inside the group, ltid its thread inside the group.
 template <class C, int LD, bool CHUNKED, bool OUT32, int SMEM>
 __device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, FastLoader<C>& ld, const RegLoader<C>& rl,
-                                            const TileFlag& tf, int64_t tm, int64_t tn, int tid, int wave, int wm,
-                                            int wn, int lane, f32x4 (&acc)[C::FM][C::FN]) {
+                                            const TileFlag& tf, int64_t tm, int64_t tn, int tid, int g, int ltid,
+                                            int lw, int wm, int wn, int lane, f32x4 (&acc)[C::FM][C::FN]) {
   const int64_t m0 = tm * C::BM, n0 = tn * C::BN;
   if (CHUNKED && kRedo) {
     // tile flag: any element of the FP32 sum inf or NaN (kernel.py:70-71)
     bool bad = false;
+    if (g == 0) {
 #pragma unroll
-    for (int i = 0; i < C::FM; ++i)
+      for (int i = 0; i < C::FM; ++i)
 #pragma unroll
-      for (int j = 0; j < C::FN; ++j)
+        for (int j = 0; j < C::FN; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) bad |= !(__builtin_fabsf(acc[i][j][r]) < __builtin_inff());
-    store_any<C, OUT32, SMEM>(p, smem, m0, n0, wave, wm, wn, lane, acc);
+          for (int r = 0; r < 4; ++r) bad |= !(__builtin_fabsf(acc[i][j][r]) < __builtin_inff());
+      store_any<C, OUT32, SMEM>(p, smem, m0, n0, lw, wm, wn, lane, acc);
+    }
     // the flag's barrier also retires every wave's reads of its LDS staging
     // slice before a redo's copies overwrite the LDS
     const int flag = tf.set_and_read(bad, lane);
@@ -1023,13 +1119,13 @@ __device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, 
 #pragma unroll
       for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (LD == kDma)
-      k_loop_fast<C, false>(p, m0, n0, 0, p.K, smem, ld, wave, wm, wn, lane, acc);
+      k_groups_fast<C, false>(p, m0, n0, 0, p.K, smem, ld, g, ltid, lw, wm, wn, lane, acc);
     else if constexpr (LD == kReg)
       k_loop_reg<C, false>(p, m0, n0, 0, p.K, smem, rl, tid, wm, wn, lane, acc);
     else
       k_loop_generic<C, false>(p, m0, n0, smem, tid, wm, wn, lane, acc);
   }
-  store_any<C, OUT32, SMEM>(p, smem, m0, n0, wave, wm, wn, lane, acc);
+  if (g == 0) store_any<C, OUT32, SMEM>(p, smem, m0, n0, lw, wm, wn, lane, acc);
 }
 
 // FP32 partials of a split tile, thread-private order: split s, block
@@ -1049,7 +1145,8 @@ __device__ __forceinline__ int part_offset(int i, int j, int tid) {
 // a v_accvgpr_read per register.
 template <class C, int LD, bool CHUNKED, bool OUT32>
 __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) void gemm_kernel(Params p) {
-  constexpr int kSmem = LD == kGather ? C::STAGE : C::NS * C::STAGE;
+  static_assert(C::KG == 1 || LD == kDma, "K groups run on the direct-to-LDS loader only");
+  constexpr int kSmem = LD == kGather ? C::STAGE : C::KG * C::RING;
   __shared__ __attribute__((aligned(1024))) char smem_raw[kSmem];
   __shared__ int tile_bad;
   char LDS_AS* smem = (char LDS_AS*)smem_raw;
@@ -1057,7 +1154,9 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) 
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+  // K group, wave and thread inside the group (KG == 1: the workgroup)
+  const int g = wave / C::NWG, lw = wave % C::NWG, ltid = tid - g * C::TG;
+  const int wm = lw / C::WAVES_N, wn = lw % C::WAVES_N;
   // block -> (tile, K split): the XCD renumbering keeps a tile's splits together
   const int64_t tiles = p.tiles_m * p.tiles_n;
   const int nsplit = C::SPLITTABLE && p.mode == kPartial ? p.splits : 1;
@@ -1080,8 +1179,8 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) 
   FastLoader<C> ld;
   RegLoader<C> rl;
   if constexpr (LD == kDma) {
-    ld.init(p, m0, n0, tid);
-    k_loop_fast<C, CHUNKED>(p, m0, n0, kbeg, kend, smem, ld, wave, wm, wn, lane, acc);
+    ld.init(p, m0, n0, ltid);
+    k_groups_fast<C, CHUNKED>(p, m0, n0, kbeg, kend, smem, ld, g, ltid, lw, wm, wn, lane, acc);
   } else if constexpr (LD == kReg) {
     rl.init(tid);
     k_loop_reg<C, CHUNKED>(p, m0, n0, kbeg, kend, smem, rl, tid, wm, wn, lane, acc);
@@ -1103,7 +1202,7 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) 
                                                part_offset<C>(i, j, 0) * 4, 0);
     return;
   }
-  finish_tile<C, LD, CHUNKED, OUT32, kSmem>(p, smem, ld, rl, tf, tm, tn, tid, wave, wm, wn, lane, acc);
+  finish_tile<C, LD, CHUNKED, OUT32, kSmem>(p, smem, ld, rl, tf, tm, tn, tid, g, ltid, lw, wm, wn, lane, acc);
 }
 
 // Split-K finishing kernel (kFinish): one workgroup per tile adds the FP32
@@ -1140,8 +1239,9 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(2))) void 
   }
   FastLoader<C> unused;
   RegLoader<C> unused_rl;
-  finish_tile<C, kGather, CHUNKED, OUT32, kSmem>(p, smem, unused, unused_rl, tf, tm, tn, tid, wave, wm, wn, lane,
-                                                 acc);
+  static_assert(C::KG == 1, "split-K tiles have one K group");
+  finish_tile<C, kGather, CHUNKED, OUT32, kSmem>(p, smem, unused, unused_rl, tf, tm, tn, tid, 0, tid, wave, wm, wn,
+                                                 lane, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -1194,19 +1294,27 @@ __global__ __launch_bounds__(256) void pack_kernel(const f16* __restrict__ src, 
 //   3   128x128  4      64x64      2 x 32 KiB    2
 //   4   128x128  4      64x64      1 x 32 KiB    generic strided gather path
 //   5   64x64    4      32x32      2 x 16 KiB    4
+//   6   128x96   2 x 4  64x48      2 x 2 x 28 KiB  1   (two K groups)
+//   7   64x32    4 x 2  32x32      4 x 3 x 12 KiB  1   (four K groups)
 template <int BL> using Cfg0 = Cfg<256, 256, 4, 2, 2, BL>;
 template <int BL> using Cfg1 = Cfg<256, 128, 4, 2, 3, BL>;
 template <int BL> using Cfg2 = Cfg<128, 256, 2, 4, 3, BL>;
 template <int BL> using Cfg3 = Cfg<128, 128, 2, 2, 2, BL>;
 template <int BL> using Cfg5 = Cfg<64, 64, 2, 2, 2, BL, 4>;
 using CfgG = Cfg<128, 128, 2, 2, 2, kKC>;
+// K-group tiles, K-contiguous b only (a row-major b's k-rows of 12 or 4
+// units do not fit the transpose-read swizzle): 128x96 as two groups of 4
+// waves of 64x48 with two-stage rings, 64x32 as four groups of 2 waves of
+// 32x32 with three-stage rings (144 KiB of LDS).
+using Cfg6 = Cfg<128, 96, 2, 2, 2, kKC, 2, 2>;
+using Cfg7 = Cfg<64, 32, 2, 1, 3, kKC, 2, 4>;
 
 struct TileInfo {
   int bm, bn, threads, per_cu;
 };
 constexpr TileInfo kTiles[F16ACC_NUM_TILES] = {
     {256, 256, 512, 1}, {256, 128, 512, 1}, {128, 256, 512, 1}, {128, 128, 256, 2}, {128, 128, 256, 2},
-    {64, 64, 256, 4}};
+    {64, 64, 256, 4},   {128, 96, 512, 1},  {64, 32, 512, 1}};
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -1306,7 +1414,19 @@ inline double rounds_256(int64_t n, int cus) {
   return (double)(n / cus) * full + (r ? full * (0.73 + 0.27 * f * f * f) : 0.0);
 }
 
-inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = nullptr) {
+// K-group tiles (kc: the operands allow them, a K-contiguous b on the fast
+// path): for small grids, the first of 128x96 (two K groups) and 64x32 (four
+// K groups) whose tiles fill more than half of the CUs in one round of one
+// workgroup per CU.  Measured on MI355X (kernel time): Qwen2.5-1.5B k/v
+// 2048x256x1536 7.96 us on 64x32 against 12.2 on 64x64 (hipBLASLt 8.7); q/o
+// 2048x1536x1536 19.5 us on 128x96 against 20.4 on 64x64; down
+// 2048x1536x8960 83.5 us on 128x96 against 87 for 128x128 split in two
+// launches.  Deeper rings in one K group ran slower (q/o 26.6 us with five
+// stages): these shapes wait on load latency, and more waves issuing loads
+// keeps more of them in flight.
+constexpr double kKGroupGain = 0.95;  // estimate of a K-group pick against the pick it replaces
+
+inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = nullptr, bool kc = false) {
   int best = 0;
   double best_t = 0;
   for (int id = 0; id < 4; ++id) {
@@ -1326,6 +1446,18 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
   // launch) nor 64x64 helps: 1024 x 4096 x 4096 on 256 tiles of 128x128
   // ran 51.7 us unsplit, 54.3 us split in two and 57.2 us on 64x64.
   if (tiles < cus) {
+    if (kc) {
+      for (int kid : {F16ACC_TILE_128x96_K2, F16ACC_TILE_64x32_K4}) {
+        const int64_t n = cdiv(M, kTiles[kid].bm) * cdiv(N, kTiles[kid].bn);
+        if (n <= cus && 2 * n > cus) {
+          if (est) {
+            choose_tile(M, N, K, cus, est, false);
+            *est *= kKGroupGain;
+          }
+          return kid;
+        }
+      }
+    }
     const TileInfo& s = kTiles[F16ACC_TILE_64x64];
     const int64_t stiles = cdiv(M, s.bm) * cdiv(N, s.bn);
     double est_best = (double)t.bm * t.bn * t.per_cu / kTileRate[best];
@@ -1373,6 +1505,8 @@ inline bool plan_tail(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak,
   const int64_t rounds = tiles / cus;
   if (rounds < 1 || tiles % cus == 0) return false;
   double whole = 0;
+  // (the estimates leave the K-group tiles out: the cuts were measured
+  // against the other tiles)
   choose_tile(M, N, K, cus, &whole);
   double best = 0.97 * whole;
   int64_t best_fill = 0;
@@ -1405,10 +1539,17 @@ struct Choice {
 };
 
 inline Choice choose(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
-                     const void* a, const void* b, int forced_tile) {
-  const int id = forced_tile >= 0 ? forced_tile : choose_tile(M, N, K, cu_count());
+                     const void* a, const void* b, int forced_tile, bool kgroups = true) {
+  int id = forced_tile >= 0 ? forced_tile
+                            : choose_tile(M, N, K, cu_count(), nullptr,
+                                          kgroups && fast_layout(N, K, sam, sak, sbk, sbn, a, b, 128, 128) == kKC);
   if (id == F16ACC_TILE_GENERIC) return Choice{id, F16ACC_FAMILY_GENERIC, kKC};
   const int bl = fast_layout(N, K, sam, sak, sbk, sbn, a, b, kTiles[id].bm, kTiles[id].bn);
+  // The K-group tiles run on the direct-to-LDS copies with a K-contiguous b
+  // only: other operands take the nearest tile without K groups (128x128,
+  // 64x64).
+  if (id == F16ACC_TILE_128x96_K2 && bl != kKC) id = F16ACC_TILE_128x128;
+  if (id == F16ACC_TILE_64x32_K4 && bl != kKC) id = F16ACC_TILE_64x64;
   if (bl >= 0) return Choice{id, F16ACC_FAMILY_FAST, bl};
   // Operands the copies cannot read: the tiles with registers to spare
   // stage them through registers (kReg); the others gather elements.  The
@@ -1480,8 +1621,12 @@ struct SplitPlan {
 
 inline SplitPlan plan_split(const Choice& ch, int64_t M, int64_t N, int64_t K, int cus) {
   SplitPlan sp{1, K, 0};
-  // 256x256 is not SPLITTABLE; 64x64 fills the GPU with its own tiles (choose_tile)
-  if (ch.family == F16ACC_FAMILY_GENERIC || ch.tile == F16ACC_TILE_256x256 || ch.tile == F16ACC_TILE_64x64) return sp;
+  // only 256x128, 128x256 and 128x128 split (SPLITTABLE: 256x256 has no
+  // registers to spare, the K-group tiles split inside the workgroup); 64x64
+  // fills the GPU with its own tiles (choose_tile)
+  if (ch.family == F16ACC_FAMILY_GENERIC ||
+      !(ch.tile == F16ACC_TILE_256x128 || ch.tile == F16ACC_TILE_128x256 || ch.tile == F16ACC_TILE_128x128))
+    return sp;
   const TileInfo& t = kTiles[ch.tile];
   const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
   if (tiles >= cus) return sp;  // every CU has a workgroup already (choose_tile)
@@ -1501,7 +1646,7 @@ inline SplitPlan plan_split(const Choice& ch, int64_t M, int64_t N, int64_t K, i
 int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* tile_flags, int64_t M, int64_t N,
               int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, int64_t scm, int64_t scn, int out_dtype,
               int chunked, void* stream, int forced_tile, void* workspace = nullptr, size_t ws_bytes = 0,
-              bool strict_ws = false) {
+              bool strict_ws = false, bool kgroups = true) {
   if (M < 0 || N < 0 || K < 0) return F16ACC_E_ARG;
   if (out_dtype != F16ACC_OUT_F16 && out_dtype != F16ACC_OUT_F32) return F16ACC_E_ARG;
   if (chunked != 0 && chunked != 1) return F16ACC_E_ARG;
@@ -1519,16 +1664,18 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
                                stream, F16ACC_TILE_256x256);
       if (rc != 0) return rc;
       return gemm_impl((const f16*)a + at * sam, b, bias, (char*)c + at * scm * esize, nullptr, M - at, N, K, sam,
-                       sak, sbk, sbn, scm, scn, out_dtype, chunked, stream, -1, workspace, ws_bytes, strict_ws);
+                       sak, sbk, sbn, scm, scn, out_dtype, chunked, stream, -1, workspace, ws_bytes, strict_ws, false);
     }
     const int rc = gemm_impl(a, b, bias, c, nullptr, M, at, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked,
                              stream, F16ACC_TILE_256x256);
     if (rc != 0) return rc;
     return gemm_impl(a, (const f16*)b + at * sbn, bias ? (const f16*)bias + at : nullptr,
                      (char*)c + at * scn * esize, nullptr, M, N - at, K, sam, sak, sbk, sbn, scm, scn, out_dtype,
-                     chunked, stream, -1, workspace, ws_bytes, strict_ws);
+                     chunked, stream, -1, workspace, ws_bytes, strict_ws, false);
   }
-  const Choice ch = choose(M, N, K, sam, sak, sbk, sbn, a, b, forced_tile);
+  // The second launch of a cut takes no K-group tile (kgroups false), so that
+  // every element sums its chunks in the single grid's order, bit for bit.
+  const Choice ch = choose(M, N, K, sam, sak, sbk, sbn, a, b, forced_tile, kgroups);
   Params p;
   p.a = (const f16*)a;
   p.b = (const f16*)b;
@@ -1568,6 +1715,8 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
       case 2: return (int)launch_fast<Cfg2>(q, ch.blayout, out32, chunked, st);
       case 3: return (int)launch_fast<Cfg3>(q, ch.blayout, out32, chunked, st);
       case 5: return (int)launch_fast<Cfg5>(q, ch.blayout, out32, chunked, st);
+      case 6: return (int)launch_cfg<Cfg6, kDma>(q, out32, chunked, st);
+      case 7: return (int)launch_cfg<Cfg7, kDma>(q, out32, chunked, st);
       default: return (int)launch_cfg<CfgG, kGather>(q, out32, chunked, st);
     }
   };
@@ -1624,7 +1773,7 @@ int scratch_ptr(void** out) {
 
 extern "C" {
 
-int f16acc_abi_version(void) { return 4; }
+int f16acc_abi_version(void) { return 5; }
 
 const char* f16acc_strerror(int code) {
   if (code == 0) return "success";

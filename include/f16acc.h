@@ -34,7 +34,11 @@ extern "C" {
 #define F16ACC_TILE_128x128 3
 #define F16ACC_TILE_GENERIC 4 /* 128x128, any strides, element gather */
 #define F16ACC_TILE_64x64 5   /* small grids: 4 waves of 32x32, 4 workgroups per CU */
-#define F16ACC_NUM_TILES 6
+#define F16ACC_TILE_128x96_K2 6 /* two K groups of 4 waves of 64x48 splitting K inside the
+                                   workgroup; K-contiguous b (else runs as 128x128) */
+#define F16ACC_TILE_64x32_K4 7  /* four K groups of 2 waves of 32x32 splitting K inside the
+                                   workgroup; K-contiguous b (else runs as 64x64) */
+#define F16ACC_NUM_TILES 8
 
 #define F16ACC_FAMILY_FAST 0    /* direct global -> LDS copies of 16-byte units */
 #define F16ACC_FAMILY_GENERIC 1 /* strided element gather through registers */
@@ -230,7 +234,7 @@ int f16acc_tail_split(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak,
 /* Short text for a return code of this library (never NULL). */
 const char* f16acc_strerror(int code);
 
-/* ABI version: bumped whenever a signature above changes. */
+/* ABI version: bumped whenever a signature or the tile ids above change. */
 int f16acc_abi_version(void);
 
 #ifdef __cplusplus

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(dll, name), name
     assert sorted(_lib.EXPORTS) == names
-    assert _lib.abi_version() == _lib.ABI_VERSION == 4
+    assert _lib.abi_version() == _lib.ABI_VERSION == 5
 
 
 def test_gemm_rejects_bad_arguments_before_launching():
@@ -122,9 +122,12 @@ class _Fake:
     (1024, 11008, 4096, (4096, 1), (1, 4096), "fast", "256x256"),  # 172 256-tiles: one partial round beats 688 128-tiles
     (2048, 2048, 1536, (1536, 1), (1, 1536), "fast", "128x128"),   # 256 128-tiles: one per CU, no 64x64 (22.8 vs 24.1 us)
     (1024, 4096, 4096, (4096, 1), (1, 4096), "fast", "128x128"),   # one per CU: no K split either (51.4 vs 54.1 us)
-    (2048, 1536, 1536, (1536, 1), (1, 1536), "fast", "64x64"),     # 192 128-tiles for 512 slots, K short
-    (2048, 256, 1536, (1536, 1), (1, 1536), "fast", "64x64"),      # Qwen k/v: 32 128-tiles
-    (2048, 1536, 8960, (8960, 1), (1, 8960), "fast", "128x128"),   # 192 128-tiles, long K: split in two
+    (2048, 1536, 1536, (1536, 1), (1, 1536), "fast", "128x96k2"),  # Qwen q/o: 256 128x96 tiles, two K groups
+    (2048, 1536, 1536, (1536, 1), (1536, 1), "fast", "64x64"),     # row-major b: no K groups; 192 128-tiles
+    (2048, 256, 1536, (1536, 1), (1, 1536), "fast", "64x32k4"),    # Qwen k/v: 256 64x32 tiles, four K groups
+    (2048, 256, 1536, (1536, 1), (256, 1), "fast", "64x64"),       # row-major b: no K groups
+    (2048, 1536, 8960, (8960, 1), (1, 8960), "fast", "128x96k2"),  # Qwen down: K groups, no second launch
+    (2048, 1536, 8960, (8960, 1), (1536, 1), "fast", "128x128"),   # row-major b: 128x128 split in two
     (128, 1536, 1536, (1536, 1), (1536, 1), "fast", "64x64"),      # 128 rows, row-major b
     (2049, 1537, 8961, (8961, 1), (1, 8961), "fast", "128x128"),   # rows not 16-byte aligned: packed first
     (300, 1537, 8961, (8961, 1), (1, 8961), "reg", "128x128"),     # read in place (cheaper than a copy)
@@ -139,12 +142,18 @@ def test_tile_table(M, N, K, sa, sb, fam, tile):
     assert cfg["tiles_m"] == -(-M // cfg["bm"]) and cfg["tiles_n"] == -(-N // cfg["bn"])
 
 
-@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic", "64x64"])
+@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic", "64x64", "128x96k2",
+                                  "64x32k4"])
 def test_forced_tile_resolves(tile):
-    bm, bn = (128, 128) if tile == "generic" else map(int, tile.split("x"))
-    cfg = tile_config(_Fake((4096, 1024), (1024, 1)), _Fake((1024, 2048), (2048, 1)), tile)
+    bm, bn = (128, 128) if tile == "generic" else (int(tile.split("x")[0]), int(tile.split("x")[1].split("k")[0]))
+    # w.t() (K-contiguous b): every tile as forced
+    cfg = tile_config(_Fake((4096, 1024), (1024, 1)), _Fake((1024, 2048), (1, 1024)), tile)
     assert cfg["tile"] == tile and (cfg["bm"], cfg["bn"]) == (bm, bn)
     assert cfg["family"] == ("generic" if tile == "generic" else "fast")
+    # a row-major b: the K-group tiles run as 128x128 and 64x64 (their K
+    # groups read a K-contiguous b only)
+    cfg = tile_config(_Fake((4096, 1024), (1024, 1)), _Fake((1024, 2048), (2048, 1)), tile)
+    assert cfg["tile"] == {"128x96k2": "128x128", "64x32k4": "64x64"}.get(tile, tile)
     # strided operands: mm packs them for a forced fast tile, so the tile holds
     cfg = tile_config(_Fake((300, 256), (512, 2)), _Fake((256, 200), (700, 3)), tile)
     assert cfg["tile"] == tile
@@ -266,9 +275,14 @@ def test_in_place_reads_only_where_they_beat_a_copy(M, N, K, in_place):
 
 def test_k_split_only_where_cus_would_idle():
     """The split-K workspace is asked for only when the pick's tiles leave some
-    CUs without a workgroup (Qwen2.5 down: 192 tiles of 128x128 for 256 CUs),
-    not when every CU already has one (1024 x 4096 x 4096: 256 tiles)."""
+    CUs without a workgroup (Qwen2.5 down with a row-major weight: 192 tiles
+    of 128x128 for 256 CUs), not when every CU already has one (1024 x 4096 x
+    4096: 256 tiles), nor where a K-group tile splits K inside the workgroup
+    (down and 2048 x 256 x 4096 with b = w.t())."""
     n = ctypes.c_size_t()
-    for (M, N, K), split in (((2048, 1536, 8960), True), ((1024, 4096, 4096), False), ((2048, 256, 4096), True)):
-        _lib.check(_lib.workspace_size(M, N, K, K, 1, 1, K, 0, 0, ctypes.byref(n)))
-        assert (n.value > 0) == split, (M, N, K)
+    for (M, N, K), b_kc, split in (((2048, 1536, 8960), False, True), ((2048, 1536, 8960), True, False),
+                                   ((1024, 4096, 4096), True, False), ((2048, 256, 4096), True, False),
+                                   ((1024, 256, 4096), True, True), ((2048, 256, 4096), False, True)):
+        sbk, sbn = (1, K) if b_kc else (N, 1)
+        _lib.check(_lib.workspace_size(M, N, K, K, 1, sbk, sbn, 0, 0, ctypes.byref(n)))
+        assert (n.value > 0) == split, (M, N, K, b_kc)

@@ -42,6 +42,27 @@ def oracle(a, b, out_dtype, cfg, chunked=True):
     return chunk32.mm(a, b, out_dtype, chunked=chunked, tile=(cfg["bm"], cfg["bn"]), return_flags=True)
 
 
+ALL_TILES = ["256x256", "256x128", "128x256", "128x128", "generic", "64x64", "128x96k2", "64x32k4"]
+
+
+# K-group tiles and the tile each runs as with a row-major b (their K groups
+# read a K-contiguous b only)
+K_GROUP_FALLBACK = {"128x96k2": "128x128", "64x32k4": "64x64"}
+
+
+def forced_tile_runs_as(tile, b_row_major):
+    """The tile a forced tile runs as."""
+    return K_GROUP_FALLBACK.get(tile, tile) if b_row_major else tile
+
+
+def tile_dims(tile):
+    """(bm, bn) of a tile name."""
+    if tile == "generic":
+        return 128, 128
+    bm, bn = tile.split("x")
+    return int(bm), int(bn.split("k")[0])
+
+
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
 @pytest.mark.parametrize("b_transposed", [False, True])
 def test_square_1024_matches_oracle_and_fp64(out_dtype, b_transposed):
@@ -219,7 +240,7 @@ def test_zero_sizes():
     assert c.shape == (64, 0)
 
 
-@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic", "64x64"])
+@pytest.mark.parametrize("tile", ALL_TILES)
 @pytest.mark.parametrize("K", [64, 128, 192, 200, 320, 1024])
 def test_every_tile_matches_oracle(tile, K):
     """Each tile configuration, forced, on ragged M/N edges, for K of one to
@@ -233,7 +254,7 @@ def test_every_tile_matches_oracle(tile, K):
     for b_t in (False, True):
         gb = b.t().contiguous().cuda().t() if b_t else b.cuda()
         cfg = tile_config(ga, gb, tile)
-        assert cfg["tile"] == tile
+        assert cfg["tile"] == forced_tile_runs_as(tile, not b_t)
         for out_dtype in (torch.float32, torch.float16):
             c, flags = mm_flags(ga, gb, out_dtype, tile=tile)
             ref, rflags = oracle(a, b, out_dtype, cfg)
@@ -243,7 +264,7 @@ def test_every_tile_matches_oracle(tile, K):
         assert rel(c32.cpu(), (a.float() @ b.float()).double()) < 1e-5
 
 
-@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic", "64x64"])
+@pytest.mark.parametrize("tile", ALL_TILES)
 def test_every_tile_stores_unaligned_rows_and_edges(tile):
     """fp16 rows of N = 517 halves start off 16-byte alignment, and M, N leave
     partial tiles: such tiles are staged through LDS and leave as 16-byte
@@ -268,7 +289,7 @@ def test_every_tile_stores_unaligned_rows_and_edges(tile):
 # Waves of each tile configuration (rows x columns of waves); wave (wm, wn)
 # owns the (bm / rows) x (bn / columns) sub-tile at (wm, wn) of its tile.
 WAVES = {"256x256": (4, 2), "256x128": (4, 2), "128x256": (2, 4), "128x128": (2, 2), "generic": (2, 2),
-         "64x64": (2, 2)}
+         "64x64": (2, 2), "128x96k2": (2, 2), "64x32k4": (2, 1)}
 
 
 def _wave_cases(tiles):
@@ -282,13 +303,12 @@ def _wave_cases(tiles):
 def _overflow_block(tile, wm, wn, ti, tj):
     """First row and column of a 10 x 10 block inside wave (wm, wn)'s
     sub-tile of output tile (ti, tj)."""
-    bm, bn = map(int, tile.split("x")) if tile != "generic" else (128, 128)
+    bm, bn = tile_dims(tile)
     wmc, wnc = WAVES[tile]
     return ti * bm + wm * (bm // wmc) + 5, tj * bn + wn * (bn // wnc) + 3
 
 
-@pytest.mark.parametrize("tile, wm, wn", _wave_cases(["256x256", "256x128", "128x256", "128x128", "generic",
-                                                      "64x64"]))
+@pytest.mark.parametrize("tile, wm, wn", _wave_cases(ALL_TILES))
 def test_every_tile_redoes_overflow_in_every_wave(tile, wm, wn):
     """Overflow closed form (reference tests/test_f16acc.py:91-101) placed in
     one wave's sub-tile of tile (1, 1) of a larger grid, for every wave of
@@ -302,14 +322,79 @@ def test_every_tile_redoes_overflow_in_every_wave(tile, wm, wn):
     b[:, c0:c0 + 10] = 0.0
     b[:32, c0:c0 + 10], b[32:64, c0:c0 + 10], b[64:96, c0:c0 + 10], b[96:, c0:c0 + 10] = 30.0, -30.0, 30.0, -30.0
     b[127, c0:c0 + 10] = -29.0
-    ga, gb = a.cuda(), b.cuda()
+    # b row-major, except for the K-group tiles, which read a K-contiguous b only
+    ga, gb = a.cuda(), (b.t().contiguous().cuda().t() if tile in K_GROUP_FALLBACK else b.cuda())
     cfg = tile_config(ga, gb, tile)
+    assert cfg["tile"] == tile
     c, flags = mm_flags(ga, gb, torch.float32, tile=tile)
     ref, rflags = oracle(a, b, torch.float32, cfg)
     assert int(rflags.sum()) == 1 and rflags[1, 1] == 1
     assert torch.equal(flags.cpu(), rflags), (tile, wm, wn)
     assert torch.all(c[r0:r0 + 10, c0:c0 + 10].cpu() == 100.0)
     assert rel(c.cpu(), ref) < TOL
+
+
+K_GROUPS = {"128x96k2": 2, "64x32k4": 4}
+
+
+@pytest.mark.parametrize("tile, wm, wn, group", [(t, wm, wn, g) for t, wm, wn in _wave_cases(list(K_GROUPS))
+                                                 for g in range(K_GROUPS[t])])
+def test_k_group_tiles_redo_overflow_in_every_group_and_wave(tile, wm, wn, group):
+    """K-group tiles split K inside the workgroup: group g sums stages
+    [2g, 2g + 2) of K = 128 * groups.  The overflow closed form (reference
+    tests/test_f16acc.py:91-101) is placed in one group's K range only (the
+    other groups' sums are exact zeros there), in one wave's sub-tile of
+    tile (1, 1): the reduced sum is NaN, so exactly that tile is flagged,
+    redone over all of K in FP32 and comes out exact; both b layouts (a
+    row-major b runs 128x96k2 as 128x128)."""
+    groups = K_GROUPS[tile]
+    M, N, K = 512, 512, 128 * groups
+    a = rnd((M, K), 40, 0.5)
+    b = rnd((K, N), 41, 0.5)
+    r0, c0 = _overflow_block(tile, wm, wn, 1, 1)
+    k0 = 128 * group
+    a[r0:r0 + 10, :] = 100.0
+    b[:, c0:c0 + 10] = 0.0
+    for q, v in enumerate((30.0, -30.0, 30.0, -30.0)):
+        b[k0 + 32 * q:k0 + 32 * q + 32, c0:c0 + 10] = v
+    b[k0 + 127, c0:c0 + 10] = -29.0
+    ga = a.cuda()
+    for b_row_major in (False, True):
+        gb = b.cuda() if b_row_major else b.t().contiguous().cuda().t()
+        cfg = tile_config(ga, gb, tile)
+        assert cfg["tile"] == forced_tile_runs_as(tile, b_row_major)
+        c, flags = mm_flags(ga, gb, torch.float32, tile=tile)
+        ref, rflags = oracle(a, b, torch.float32, cfg)
+        assert int(rflags.sum()) == 1 and rflags[r0 // cfg["bm"], c0 // cfg["bn"]] == 1
+        assert torch.equal(flags.cpu(), rflags), (tile, wm, wn, group, b_row_major)
+        assert torch.all(c[r0:r0 + 10, c0:c0 + 10].cpu() == 100.0)
+        assert rel(c.cpu(), ref) < TOL
+
+
+@pytest.mark.parametrize("tile", list(K_GROUPS))
+@pytest.mark.parametrize("K", [0, 8, 64, 72, 136, 200, 448, 1536, 1560])
+def test_k_group_tiles_with_uneven_and_empty_groups(tile, K):
+    """K ranges that leave the last K groups with fewer stages or none
+    (K = 64 on four groups: one stage; K = 0: none at all), a partial last
+    stage, fp16 and fp32 out, chunked and FP32 modes, against the oracle."""
+    from f16acc_amd.kernel import mm_tile
+
+    M, N = 200, 136
+    a, b = rnd((M, K), 50 + K), rnd((K, N), 51 + K)
+    ga, gb = a.cuda(), b.t().contiguous().cuda().t()
+    cfg = tile_config(ga, gb, tile)
+    assert cfg["tile"] == tile or K == 0  # K = 0: no layout to read, any tile
+    for out_dtype in (torch.float32, torch.float16):
+        c, flags = mm_flags(ga, gb, out_dtype, tile=tile)
+        ref, rflags = oracle(a, b, out_dtype, cfg)
+        assert torch.equal(flags.cpu(), rflags)
+        if K == 0:
+            assert bool((c == 0).all())
+        else:
+            assert rel(c.cpu(), ref) < TOL, (tile, K, out_dtype)
+    c32 = mm_tile(ga, gb, tile, torch.float32, chunked=False)
+    if K:
+        assert rel(c32.cpu(), (a.float() @ b.float()).double()) < 1e-5
 
 
 def _packed_case(a, b):
@@ -514,7 +599,7 @@ def _split_plan(ga, gb):
     return n.value
 
 
-@pytest.mark.parametrize("shape", [(256, 256, 4096), (2048, 256, 4096), (300, 200, 4200), (512, 384, 8960)])
+@pytest.mark.parametrize("shape", [(256, 256, 4096), (1024, 256, 4096), (300, 200, 4200), (512, 384, 8960)])
 def test_split_k_matches_oracle(shape):
     """Shapes with few output tiles are split along K into chunk-aligned
     ranges; a second launch adds the FP32 partials per tile.  Results and
@@ -588,25 +673,25 @@ def test_split_k_overflow_in_every_wave_of_a_split_tile(tile, wm, wn):
 
 
 def test_split_k_bias_and_ws_entry_without_workspace():
-    """A biased projection with few output tiles and long K (2048 x 256 x
+    """A biased projection with few output tiles and long K (1024 x 256 x
     4096) takes the split path through patch.linear and still equals the
     unfused y = mm(x2, w.t()); y += b bit for bit; f16acc_gemm_ws with no
     workspace is f16acc_gemm."""
     from f16acc_amd import _lib, patch
 
-    x, w, bias = rnd((2048, 4096), 72).cuda(), rnd((256, 4096), 73, 0.02).cuda(), rnd((256,), 74, 0.02).cuda()
+    x, w, bias = rnd((1024, 4096), 72).cuda(), rnd((256, 4096), 73, 0.02).cuda(), rnd((256,), 74, 0.02).cuda()
     assert _split_plan(x, w.t()) > 0
     unfused = f16acc.mm(x, w.t())
     unfused += bias
     with torch.no_grad():
         assert torch.equal(patch.linear(x, w, bias), unfused)
-    c = torch.empty(2048, 256, device="cuda", dtype=torch.float16)
+    c = torch.empty(1024, 256, device="cuda", dtype=torch.float16)
     st = torch.cuda.current_stream().cuda_stream
-    rc = _lib.gemm_ws(x.data_ptr(), w.data_ptr(), None, c.data_ptr(), None, 2048, 256, 4096, x.stride(0), 1,
+    rc = _lib.gemm_ws(x.data_ptr(), w.data_ptr(), None, c.data_ptr(), None, 1024, 256, 4096, x.stride(0), 1,
                       1, 4096, 256, 1, 0, 1, st, None, 0)
     assert rc == 0
     plain = torch.empty_like(c)
-    assert _lib.gemm(x.data_ptr(), w.data_ptr(), plain.data_ptr(), None, 2048, 256, 4096, x.stride(0), 1, 1, 4096,
+    assert _lib.gemm(x.data_ptr(), w.data_ptr(), plain.data_ptr(), None, 1024, 256, 4096, x.stride(0), 1, 1, 4096,
                      256, 1, 0, 1, st) == 0
     assert torch.equal(c, plain)
     assert rel(c.cpu(), chunk32.mm(x.cpu(), w.cpu().t(), torch.float16, tile=(128, 128))) < TOL
@@ -810,19 +895,21 @@ def test_graph_keeps_its_split_k_workspace_when_a_larger_one_replaces_it():
     across replays, and every replay still equals the eager result."""
     from f16acc_amd import kernel
 
-    x1, w1 = rnd((2048, 4096), 110).cuda(), rnd((256, 4096), 111, 0.02).cuda()  # 8 MiB of partials
-    x2, w2 = rnd((1024, 16384), 112).cuda(), rnd((512, 16384), 113, 0.02).cuda()  # 32 MiB
-    eager1 = f16acc.mm(x1, w1.t())
+    # weights row-major [K, N] (b = w.t() would split K inside the workgroup
+    # on these shapes, with no workspace)
+    x1, w1 = rnd((2048, 4096), 110).cuda(), rnd((4096, 256), 111, 0.02).cuda()  # 8 MiB of partials
+    x2, w2 = rnd((1024, 16384), 112).cuda(), rnd((16384, 512), 113, 0.02).cuda()  # 32 MiB
+    eager1 = f16acc.mm(x1, w1)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     key = (x1.device.index, side.cuda_stream)
     with torch.cuda.stream(side):
-        f16acc.mm(x1, w1.t())  # the workspace exists before capture
+        f16acc.mm(x1, w1)  # the workspace exists before capture
         captured = kernel._workspaces[key]
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=side):
-            out = f16acc.mm(x1, w1.t())
-        eager2 = f16acc.mm(x2, w2.t())
+            out = f16acc.mm(x1, w1)
+        eager2 = f16acc.mm(x2, w2)
         assert kernel._workspaces[key] is not captured and kernel._workspaces[key].numel() > captured.numel()
         victim = torch.full((captured.numel(),), 0x5A, dtype=torch.uint8, device="cuda")
     torch.cuda.synchronize()
@@ -831,7 +918,7 @@ def test_graph_keeps_its_split_k_workspace_when_a_larger_one_replaces_it():
         torch.cuda.synchronize()
         assert torch.equal(out, eager1)
         assert bool((victim == 0x5A).all())
-    assert torch.equal(f16acc.mm(x2, w2.t()), eager2)
+    assert torch.equal(f16acc.mm(x2, w2), eager2)
 
 
 def _random_operand(g, rows, cols, kind, seed):

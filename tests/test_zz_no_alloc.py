@@ -58,14 +58,17 @@ def test_noalloc_equals_workspace_entry_on_two_calls_in_a_row():
     from f16acc_amd.kernel import tile_config
 
     ws = torch.empty(32 << 20, dtype=torch.uint8, device="cuda")
-    # call 1: Qwen2.5-1.5B down projection (2048 x 1536 x 8960, w.t(), fused
-    # bias, fp16 out), split in two on 128x128 tiles (25.2 MB of partials)
+    # call 1: the Qwen2.5-1.5B down projection's shape (2048 x 1536 x 8960,
+    # fused bias, fp16 out) with the weight row-major [K, N] (b = w.t() would
+    # split K inside the workgroup instead), split in two on 128x128 tiles
+    # (25.2 MB of partials)
     x, w, bias = rnd((2048, 8960), 82).cuda(), rnd((1536, 8960), 83, 0.02).cuda(), rnd((1536,), 84, 0.02).cuda()
+    w_kn = w.t().contiguous()
     # call 2, smaller: 256 x 256 x 4096 (b row-major, fp32 out) with an
     # overflow in one split, split four ways
     oa, ob = _overflow_case()
     ga, gb = oa.cuda(), ob.cuda()
-    cases = [(x, w.t(), bias, torch.float16), (ga, gb, None, torch.float32)]
+    cases = [(x, w_kn, bias, torch.float16), (ga, gb, None, torch.float32)]
     for i, (a, b, bi, dt) in enumerate(cases):
         assert _split_bytes(a, b) > 0, "expected a split-K plan"
         cfg = tile_config(a, b)
@@ -92,9 +95,9 @@ def test_noalloc_equals_workspace_entry_on_two_calls_in_a_row():
     from f16acc_amd.kernel import mm_bias
 
     again = torch.empty(2048, 1536, device="cuda", dtype=torch.float16)
-    _call(_lib.gemm_noalloc, x, w.t(), bias, again, None)
+    _call(_lib.gemm_noalloc, x, w_kn, bias, again, None)
     torch.cuda.synchronize()
-    assert torch.equal(again, mm_bias(x, w.t(), bias))
+    assert torch.equal(again, mm_bias(x, w_kn, bias))
 
 
 def test_noalloc_unsplit_problem_equals_plain_entry():
