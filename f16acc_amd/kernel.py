@@ -30,9 +30,14 @@ _FAMILIES = ("fast", "generic", "reg")
 # share it.  A workspace that a larger one replaces is kept, not freed: a HIP
 # graph captured earlier holds its address and writes there on every replay,
 # so its memory must never go to another tensor.  Sizes grow at least 2x, so
-# few are kept.
+# few are kept.  A call under HIP graph capture gets the workspace of its
+# capture (device, stream, capture id), used by no eager call and no other
+# graph, so replays of different graphs, on any streams, and eager calls on
+# the capture stream never share partials; it is kept for the life of the
+# process, as the graph may be replayed at any time.
 _workspaces = {}
 _retired = []
+_hip = None  # libamdhip64, for hipStreamGetCaptureInfo
 _ws_sizes = {}  # problem key -> f16acc_workspace_size result
 _WS_MEMO_MAX = 4096
 
@@ -84,6 +89,8 @@ def _workspace(a, b, M, N, K):
     if nbytes == 0:
         return None
     skey = (a.device.index, _stream(a.device))
+    if torch.cuda.is_current_stream_capturing():
+        skey += (_capture_id(skey[1]),)
     ws = _workspaces.get(skey)
     if ws is None or ws.numel() < nbytes:
         if ws is not None:
@@ -92,6 +99,22 @@ def _workspace(a, b, M, N, K):
         ws = torch.empty(max(nbytes, grown, 1 << 20), dtype=torch.uint8, device=a.device)
         _workspaces[skey] = ws
     return ws
+
+
+def _capture_id(stream):
+    """Sequence id of the HIP graph capture running on `stream`
+    (hipStreamGetCaptureInfo); a fresh key where the runtime will not say, so
+    that such a call gets a workspace of its own."""
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so")
+        _hip.hipStreamGetCaptureInfo.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int),
+                                                 ctypes.POINTER(ctypes.c_ulonglong)]
+        _hip.hipStreamGetCaptureInfo.restype = ctypes.c_int
+    status, cid = ctypes.c_int(), ctypes.c_ulonglong()
+    if _hip.hipStreamGetCaptureInfo(stream, ctypes.byref(status), ctypes.byref(cid)) != 0 or status.value != 1:
+        return object()  # hipStreamCaptureStatusActive is 1
+    return cid.value
 
 
 def mm_bias(a, b, bias, out_dtype=torch.float16, chunked=True):

@@ -921,6 +921,39 @@ def test_graph_keeps_its_split_k_workspace_when_a_larger_one_replaces_it():
     assert torch.equal(f16acc.mm(x2, w2), eager2)
 
 
+def test_graphs_captured_on_one_stream_get_their_own_split_k_workspaces():
+    """torch.cuda.graph captures on one shared side stream by default.  Two
+    graphs with a split-K mm each get a workspace of their own, distinct from
+    the eager one, so replaying both at once on two streams while an eager
+    split-K call runs cannot mix their FP32 partials: every replay equals the
+    eager result, bit for bit."""
+    from f16acc_amd import kernel
+
+    # weights row-major [K, N]: 2048 x 256 x 4096 splits K (8 MiB of partials)
+    x1, w1 = rnd((2048, 4096), 120).cuda(), rnd((4096, 256), 121, 0.02).cuda()
+    x2, w2 = rnd((2048, 4096), 122).cuda(), rnd((4096, 256), 123, 0.02).cuda()
+    e1, e2 = f16acc.mm(x1, w1), f16acc.mm(x2, w2)
+    before = {id(t) for t in kernel._workspaces.values()}
+    g1, g2 = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1):
+        o1 = f16acc.mm(x1, w1)
+    with torch.cuda.graph(g2):
+        o2 = f16acc.mm(x2, w2)
+    new = [t for t in kernel._workspaces.values() if id(t) not in before]
+    assert len(new) == 2 and new[0].data_ptr() != new[1].data_ptr()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for _ in range(3):
+        s1.wait_stream(torch.cuda.current_stream())
+        s2.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s1):
+            g1.replay()
+        with torch.cuda.stream(s2):
+            g2.replay()
+        e3 = f16acc.mm(x1, w1)  # eager, at the same time, on the current stream
+        torch.cuda.synchronize()
+        assert torch.equal(o1, e1) and torch.equal(o2, e2) and torch.equal(e3, e1)
+
+
 def _random_operand(g, rows, cols, kind, seed):
     """A [rows, cols] fp16 CPU tensor laid out as `kind` (its GPU twin has the
     same strides): contiguous, transposed view, strided view or offset view."""
