@@ -1415,15 +1415,20 @@ inline double rounds_256(int64_t n, int cus) {
 }
 
 // K-group tiles (kc: the operands allow them, a K-contiguous b on the fast
-// path): for small grids, the first of 128x96 (two K groups) and 64x32 (four
-// K groups) whose tiles fill more than half of the CUs in one round of one
-// workgroup per CU.  Measured on MI355X (kernel time): Qwen2.5-1.5B k/v
-// 2048x256x1536 7.96 us on 64x32 against 12.2 on 64x64 (hipBLASLt 8.7); q/o
-// 2048x1536x1536 19.5 us on 128x96 against 20.4 on 64x64; down
-// 2048x1536x8960 83.5 us on 128x96 against 87 for 128x128 split in two
-// launches.  Deeper rings in one K group ran slower (q/o 26.6 us with five
-// stages): these shapes wait on load latency, and more waves issuing loads
-// keeps more of them in flight.
+// path), for small grids: 128x96 (two K groups) where its tiles fill more
+// than half of the CUs in one round of one workgroup per CU, else 64x32 (four
+// K groups) where its tiles fit in one round at all.  Measured on MI355X:
+// Qwen2.5-1.5B k/v 2048x256x1536 7.96 us on 64x32 against 12.2 on 64x64
+// (kernel time; hipBLASLt 8.7); q/o 2048x1536x1536 19.5 us on 128x96 against
+// 20.4 on 64x64; down 2048x1536x8960 83.5 us on 128x96 against 87 for
+// 128x128 split in two launches; llama-2-7B gate/up at 256 tokens 39.4 us on
+// 128x96 against 42.9 on 64x64 (per call).  Short-M, long-K projections
+// with few tiles gain most from four groups: llama-3-8B k/v at 256 tokens
+// (256x1024x4096, 128 tiles) 13.0 us against 19.9 for 128x128 split in two
+// launches, Qwen2.5-7B k/v (256x512x3584, 64 tiles) 11.8 against 20.9.  At
+// two rounds 64x32 only ties the split (256x4096x4096: 25.1 against 25.2
+// us), so it stops at one.  Deeper rings in one K group ran slower (q/o 26.6
+// us with five stages), and so did register-staged loads two stages ahead.
 constexpr double kKGroupGain = 0.95;  // estimate of a K-group pick against the pick it replaces
 
 inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = nullptr, bool kc = false) {
@@ -1447,15 +1452,15 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
   // ran 51.7 us unsplit, 54.3 us split in two and 57.2 us on 64x64.
   if (tiles < cus) {
     if (kc) {
-      for (int kid : {F16ACC_TILE_128x96_K2, F16ACC_TILE_64x32_K4}) {
-        const int64_t n = cdiv(M, kTiles[kid].bm) * cdiv(N, kTiles[kid].bn);
-        if (n <= cus && 2 * n > cus) {
-          if (est) {
-            choose_tile(M, N, K, cus, est, false);
-            *est *= kKGroupGain;
-          }
-          return kid;
+      const int64_t n2 = cdiv(M, kTiles[F16ACC_TILE_128x96_K2].bm) * cdiv(N, kTiles[F16ACC_TILE_128x96_K2].bn);
+      const int64_t n4 = cdiv(M, kTiles[F16ACC_TILE_64x32_K4].bm) * cdiv(N, kTiles[F16ACC_TILE_64x32_K4].bn);
+      const int kid = n2 <= cus && 2 * n2 > cus ? F16ACC_TILE_128x96_K2 : n4 <= cus ? F16ACC_TILE_64x32_K4 : -1;
+      if (kid >= 0) {
+        if (est) {
+          choose_tile(M, N, K, cus, est, false);
+          *est *= kKGroupGain;
         }
+        return kid;
       }
     }
     const TileInfo& s = kTiles[F16ACC_TILE_64x64];
