@@ -242,56 +242,74 @@ __device__ __forceinline__ void wait_vm0() { wait_vm<0>(); }
 // ---------------------------------------------------------------------------
 // Per-thread stage loader state for the direct-to-LDS fast path.
 // ---------------------------------------------------------------------------
+// Buffer resource r moved `off` bytes up (off >= 0), its record count
+// lowered to match (0 if nothing is left): every value stays in scalar
+// registers, so a unit's copy needs no per-lane address arithmetic.
+__device__ __forceinline__ i32x4 srd_at(const i32x4& r, int off) {
+  i32x4 q = r;
+  const uint64_t base = (((uint64_t)(uint32_t)r[1] << 32) | (uint32_t)r[0]) + (uint32_t)off;
+  q[0] = (int)(uint32_t)base;
+  q[1] = (int)(uint32_t)(base >> 32);
+  q[2] = r[2] > off ? r[2] - off : 0;
+  return q;
+}
+
 template <class C>
 struct FastLoader {
   // Unit j of a thread sits j * RA rows (A, KC b) or j * RB k-rows (NC b)
   // below its unit 0, at the same swizzled column (the swizzles repeat
-  // every 16 rows; RA and RB are multiples of 16), so a thread keeps unit 0
-  // only: byte offsets inside the stage's rebased windows, first k (KC) or
-  // k-row (NC), and how many rows below unit 0 stay inside M (N for a KC b).
+  // every 16 rows; RA and RB are multiples of 16).  A unit's copy reads a
+  // resource whose base is moved down to unit j's first row (scalar
+  // registers) at the thread's unit-0 byte offset, so the per-lane offset is
+  // one register per operand and stage.  Rows past M (past N for a KC b; k
+  // rows past the stage's K range for an NC b) lie beyond the resource's
+  // record count and read zeros; units past the stage's K range (KC) and
+  // units whose columns lie past N (NC) take the offset kOob.
   static constexpr int RA = C::TG / 8, RB = C::BL == kKC ? C::TG / 8 : C::TG / C::UB;
   static_assert(RA % 16 == 0 && RB % 16 == 0, "unit rows must keep the swizzle phase");
-  int a_off, a_k, a_left;
-  int b_off, b_k, b_left;
+  int a_off, a_k;  // unit 0 of A: byte offset in the stage window, first k
+  int b_off, b_k;  // unit 0 of b: byte offset; first k (KC) or k-row (NC)
+  int b_col;       // NC: b_off, or kOob where the unit's columns lie past N
   int a_step, b_step;  // bytes between consecutive units (wave-uniform)
+  int a_rec, b_rec;    // records (bytes) of the tile's rows inside M / N (KC b), wave-uniform
 
   __device__ __forceinline__ void init(const Params& p, int64_t m0, int64_t n0, int tid) {
     const int row = tid >> 3, u = (tid & 7) ^ kc_swz(row);
     a_off = (int)(row * p.sam * 2 + u * 16);
     a_k = 8 * u;
-    a_left = (int)(p.M - m0 - row < C::BM ? p.M - m0 - row : C::BM);
     a_step = __builtin_amdgcn_readfirstlane((int)(RA * p.sam * 2));
+    const int64_t ar = (p.M - m0) * p.sam * 2;
+    a_rec = __builtin_amdgcn_readfirstlane((int)(ar < kOob ? ar : kOob));
     if (C::BL == kKC) {
       const int brow = tid >> 3, bu = (tid & 7) ^ kc_swz(brow);
       b_off = (int)(brow * p.sbn * 2 + bu * 16);
       b_k = 8 * bu;
-      b_left = (int)(p.N - n0 - brow < C::BN ? p.N - n0 - brow : C::BN);
       b_step = __builtin_amdgcn_readfirstlane((int)(RB * p.sbn * 2));
+      const int64_t br = (p.N - n0) * p.sbn * 2;
+      b_rec = __builtin_amdgcn_readfirstlane((int)(br < kOob ? br : kOob));
+      b_col = b_off;
     } else {
       const int krow = tid / C::UB, bu = (tid % C::UB) ^ (nc_swz(krow) & (C::UB - 1));
       b_off = (int)(krow * p.sbk * 2 + bu * 16);
       b_k = krow;
-      b_left = n0 + 8 * bu < p.N ? kStageK : 0;  // the unit's columns inside N: every k-row, else none
       b_step = __builtin_amdgcn_readfirstlane((int)(RB * p.sbk * 2));
+      b_rec = 0;  // per stage: the stage's k-rows inside K
+      b_col = n0 + 8 * bu < p.N ? b_off : kOob;
     }
   }
 
   // The copies of one stage (k from kbase): unit(j) issues this thread's
   // j-th 16-byte copy, j < LA + LB (A units first).
   struct Stage {
-    i32x4 ra, rb;
-    int lds, krem;
+    i32x4 ra, rb;  // unit-0 resources of the stage
+    int va, vb;    // this lane's offsets for the stage
+    int lds;
     const FastLoader* ld;
     __device__ __forceinline__ void unit(int j) const {
-      if (j < C::LA) {
-        const bool ok = j * RA < ld->a_left && ld->a_k < krem;
-        lds_dma16(ra, lds + j * C::TG * 16, ok ? ld->a_off + j * ld->a_step : kOob);
-      } else {
-        const int jb = j - C::LA;
-        const bool ok = C::BL == kKC ? jb * RB < ld->b_left && ld->b_k < krem
-                                     : ld->b_k + jb * RB < krem && jb * RB < ld->b_left;
-        lds_dma16(rb, lds + C::A_STAGE + jb * C::TG * 16, ok ? ld->b_off + jb * ld->b_step : kOob);
-      }
+      if (j < C::LA)
+        lds_dma16(srd_at(ra, j * ld->a_step), lds + j * C::TG * 16, va);
+      else
+        lds_dma16(srd_at(rb, (j - C::LA) * ld->b_step), lds + C::A_STAGE + (j - C::LA) * C::TG * 16, vb);
     }
     __device__ __forceinline__ void all() const {
 #pragma unroll
@@ -302,10 +320,20 @@ struct FastLoader {
   __device__ __forceinline__ Stage stage(const Params& p, int64_t m0, int64_t n0, int64_t kbase, int64_t kend, char LDS_AS* slot,
                          int wave) const {
     Stage st;
-    const int64_t krem = kend - kbase;  // k < krem is inside this workgroup's K range
-    st.krem = krem < kStageK ? (int)krem : kStageK;
+    const int64_t kr = kend - kbase;  // k < kr is inside this workgroup's K range
+    const int krem = kr < kStageK ? (kr > 0 ? (int)kr : 0) : kStageK;
     st.ra = make_srd(p.a + (m0 * p.sam + kbase));
-    st.rb = C::BL == kKC ? make_srd(p.b + (n0 * p.sbn + kbase)) : make_srd(p.b + (kbase * p.sbk + n0));
+    st.ra[2] = a_rec;
+    st.va = a_k < krem ? a_off : kOob;
+    if (C::BL == kKC) {
+      st.rb = make_srd(p.b + (n0 * p.sbn + kbase));
+      st.rb[2] = b_rec;
+      st.vb = b_k < krem ? b_off : kOob;
+    } else {
+      st.rb = make_srd(p.b + (kbase * p.sbk + n0));
+      st.rb[2] = __builtin_amdgcn_readfirstlane(krem * (int)p.sbk * 2);  // k-rows inside K
+      st.vb = b_col;
+    }
     st.lds = __builtin_amdgcn_readfirstlane((int)(uint32_t)(size_t)slot + wave * 64 * 16);
     st.ld = this;
     return st;
