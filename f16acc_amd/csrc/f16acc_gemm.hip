@@ -639,10 +639,16 @@ __device__ __forceinline__ int64_t group_range(int64_t kbeg, int64_t kend, int g
 // (((S_0 + S_1) + S_2) + ...: deterministic).  Groups 1..KG-1 park their
 // sums in the LDS (free: every K loop ends with a barrier), one 16-byte unit
 // per thread and block, consecutive threads on consecutive units.  Ends with
-// a barrier, so the LDS is free again for the store's staging.
+// a barrier, so the LDS is free again for the store's staging.  With `flag`
+// (the chunked pass), thread 0 clears the tile's flag word before the first
+// barrier and group 0 raises it before the last one when its sum holds inf
+// or NaN (kernel.py:70-71), so every wave reads the flag after it with no
+// barrier of its own.
 template <class C>
-__device__ __forceinline__ void group_reduce(char LDS_AS* smem, int g, int ltid, f32x4 (&acc)[C::FM][C::FN]) {
+__device__ __forceinline__ void group_reduce(char LDS_AS* smem, int g, int ltid, f32x4 (&acc)[C::FM][C::FN],
+                                             int LDS_AS* flag = nullptr) {
   if constexpr (C::KG > 1) {
+    if (flag && ltid == 0 && g == 0) *flag = 0;  // the first barrier orders this before any raise
     if (g > 0) {
       char LDS_AS* mine = smem + (g - 1) * (C::BM * C::BN * 4);
 #pragma unroll
@@ -661,6 +667,16 @@ __device__ __forceinline__ void group_reduce(char LDS_AS* smem, int g, int ltid,
           for (int j = 0; j < C::FN; ++j)
             acc[i][j] += *(const f32x4 LDS_AS*)(theirs + ((i * C::FN + j) * C::TG + ltid) * 16);
       }
+      if (flag) {
+        bool bad = false;
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+          for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) bad |= !(__builtin_fabsf(acc[i][j][r]) < __builtin_inff());
+        if (__builtin_amdgcn_ballot_w64(bad) != 0 && (ltid & 63) == 0) *flag = 1;
+      }
     }
     __syncthreads();
   }
@@ -671,11 +687,12 @@ __device__ __forceinline__ void group_reduce(char LDS_AS* smem, int g, int ltid,
 template <class C, bool CHUNKED>
 __device__ __forceinline__ void k_groups_fast(const Params& p, int64_t m0, int64_t n0, int64_t kbeg, int64_t kend,
                                               char LDS_AS* smem, FastLoader<C>& ld, int g, int ltid, int lw, int wm,
-                                              int wn, int lane, f32x4 (&acc)[C::FM][C::FN]) {
+                                              int wn, int lane, f32x4 (&acc)[C::FM][C::FN],
+                                              int LDS_AS* flag = nullptr) {
   int64_t gbeg = kbeg, gend = kend, iters = 0;
   if (C::KG > 1) iters = group_range<C>(kbeg, kend, g, &gbeg, &gend);
   k_loop_fast<C, CHUNKED>(p, m0, n0, gbeg, gend, smem + g * C::RING, ld, lw, wm, wn, lane, acc, iters);
-  group_reduce<C>(smem, g, ltid, acc);
+  group_reduce<C>(smem, g, ltid, acc, flag);
 }
 
 // ---------------------------------------------------------------------------
@@ -1124,7 +1141,20 @@ __device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, 
                                             const TileFlag& tf, int64_t tm, int64_t tn, int tid, int g, int ltid,
                                             int lw, int wm, int wn, int lane, f32x4 (&acc)[C::FM][C::FN]) {
   const int64_t m0 = tm * C::BM, n0 = tn * C::BN;
-  if (CHUNKED && kRedo) {
+  if constexpr (CHUNKED && kRedo && C::KG > 1) {
+    // the flag word was raised before group_reduce's last barrier: no store
+    // to repeat for a clean tile, no barrier of its own
+    const int flag = *tf.word;
+    if (p.flags && tid == 0) p.flags[tm * p.tiles_n + tn] = (uint8_t)flag;
+    if (__builtin_expect(flag, 0)) {
+      // redo the whole tile, all of K, with FP32 accumulation (kernel.py:75-81)
+#pragma unroll
+      for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      k_groups_fast<C, false>(p, m0, n0, 0, p.K, smem, ld, g, ltid, lw, wm, wn, lane, acc);
+    }
+  } else if constexpr (CHUNKED && kRedo) {
     // tile flag: any element of the FP32 sum inf or NaN (kernel.py:70-71)
     bool bad = false;
     if (g == 0) {
@@ -1140,7 +1170,7 @@ __device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, 
     // slice before a redo's copies overwrite the LDS
     const int flag = tf.set_and_read(bad, lane);
     if (p.flags && tid == 0) p.flags[tm * p.tiles_n + tn] = (uint8_t)flag;
-    if (!flag) return;
+    if (__builtin_expect(!flag, 1)) return;
     // redo the whole tile, all of K, with FP32 accumulation (kernel.py:75-81)
 #pragma unroll
     for (int i = 0; i < C::FM; ++i)
@@ -1196,7 +1226,7 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) 
   const int64_t m0 = tm * C::BM, n0 = tn * C::BN;
   const int64_t kbeg = nsplit > 1 ? split * p.kps : 0;
   const int64_t kend = nsplit > 1 && kbeg + p.kps < p.K ? kbeg + p.kps : p.K;
-  if (CHUNKED && kRedo && p.mode != kPartial) tf.clear(tid);
+  if (CHUNKED && kRedo && p.mode != kPartial && C::KG == 1) tf.clear(tid);  // K groups: in group_reduce
 
   f32x4 acc[C::FM][C::FN];
 #pragma unroll
@@ -1208,7 +1238,8 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) 
   RegLoader<C> rl;
   if constexpr (LD == kDma) {
     ld.init(p, m0, n0, ltid);
-    k_groups_fast<C, CHUNKED>(p, m0, n0, kbeg, kend, smem, ld, g, ltid, lw, wm, wn, lane, acc);
+    k_groups_fast<C, CHUNKED>(p, m0, n0, kbeg, kend, smem, ld, g, ltid, lw, wm, wn, lane, acc,
+                              CHUNKED && kRedo && C::KG > 1 ? tf.word : nullptr);
   } else if constexpr (LD == kReg) {
     rl.init(tid);
     k_loop_reg<C, CHUNKED>(p, m0, n0, kbeg, kend, smem, rl, tid, wm, wn, lane, acc);
