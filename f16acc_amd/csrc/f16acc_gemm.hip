@@ -1485,10 +1485,17 @@ inline double rounds_256(int64_t n, int cus) {
 // with few tiles gain most from four groups: llama-3-8B k/v at 256 tokens
 // (256x1024x4096, 128 tiles) 13.0 us against 19.9 for 128x128 split in two
 // launches, Qwen2.5-7B k/v (256x512x3584, 64 tiles) 11.8 against 20.9.  At
-// two rounds 64x32 only ties the split (256x4096x4096: 25.1 against 25.2
-// us), so it stops at one.  Deeper rings in one K group ran slower (q/o 26.6
-// us with five stages), and so did register-staged loads two stages ahead.
+// two rounds 64x32 is weighed against the other tiles' estimate (a 128x128
+// K split, 64x64): one round of it costs kKGroup4Round, in those units, which
+// ties a 128x128 split in four (256x4096x4096: 25.5 against 25.7 us), beats
+// a split in three (256x3584x3584: 22.7 against 24.4 us) and loses to a
+// split in eight (256x4096x11008: 61.3 against 45.8 us); a tie takes 64x32,
+// which needs neither a second launch nor a workspace.  Deeper rings in one
+// K group ran slower (q/o 26.6 us with five stages), and so did
+// register-staged loads two stages ahead.
 constexpr double kKGroupGain = 0.95;  // estimate of a K-group pick against the pick it replaces
+// half of a 128x128 round (two workgroups per CU) split in four
+constexpr double kKGroup4Round = 128.0 * 128.0 * 2 / kTileRate[F16ACC_TILE_128x128] / 8 * kSplitCost;
 
 inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = nullptr, bool kc = false) {
   int best = 0;
@@ -1520,6 +1527,14 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
           *est *= kKGroupGain;
         }
         return kid;
+      }
+      if (n4 <= 2 * (int64_t)cus) {
+        double other = 0;
+        choose_tile(M, N, K, cus, &other, false);
+        if (2 * kKGroup4Round <= other * 1.001) {
+          if (est) *est = 2 * kKGroup4Round;
+          return F16ACC_TILE_64x32_K4;
+        }
       }
     }
     const TileInfo& s = kTiles[F16ACC_TILE_64x64];

@@ -128,7 +128,11 @@ class _Fake:
     (2048, 256, 1536, (1536, 1), (256, 1), "fast", "64x64"),       # row-major b: no K groups
     (256, 1024, 4096, (4096, 1), (1, 4096), "fast", "64x32k4"),    # llama-3-8B k/v, 256 tokens: 128 tiles
     (256, 512, 3584, (3584, 1), (1, 3584), "fast", "64x32k4"),     # Qwen2.5-7B k/v, 256 tokens: 64 tiles
-    (256, 4096, 4096, (4096, 1), (1, 4096), "fast", "128x128"),    # 512 64x32 tiles: two rounds, split instead
+    (256, 4096, 4096, (4096, 1), (1, 4096), "fast", "64x32k4"),    # 512 64x32 tiles: two rounds tie a split in four
+    (1024, 1024, 4096, (4096, 1), (1, 4096), "fast", "64x32k4"),   # llama-3-8B k/v, 1024 tokens: two rounds
+    (256, 3584, 3584, (3584, 1), (1, 3584), "fast", "64x32k4"),    # Qwen2.5-7B q/o, 256 tokens: beats a split in three
+    (256, 4096, 5120, (5120, 1), (1, 5120), "fast", "128x128"),    # two rounds of 64x32 lose to a split in five
+    (256, 4096, 11008, (11008, 1), (1, 11008), "fast", "128x128"), # llama-2-7B down, 256 tokens: split in eight
     (256, 11008, 4096, (4096, 1), (1, 4096), "fast", "128x96k2"),  # llama-2-7B gate/up, 256 tokens: 230 tiles
     (2048, 1536, 8960, (8960, 1), (1, 8960), "fast", "128x96k2"),  # Qwen down: K groups, no second launch
     (2048, 1536, 8960, (8960, 1), (1536, 1), "fast", "128x128"),   # row-major b: 128x128 split in two
@@ -282,13 +286,15 @@ def test_k_split_only_where_cus_would_idle():
     CUs without a workgroup (Qwen2.5 down with a row-major weight: 192 tiles
     of 128x128 for 256 CUs), not when every CU already has one (1024 x 4096 x
     4096: 256 tiles), nor where a K-group tile splits K inside the workgroup
-    (down, 2048 x 256 x 4096 and 1024 x 256 x 4096 with b = w.t()); 256 x
-    4096 x 4096 would need two rounds of 64x32 tiles, so it splits."""
+    (down, 2048 x 256 x 4096, 1024 x 256 x 4096 and 256 x 4096 x 4096 with
+    b = w.t(), the last on two rounds of 64x32 tiles); 256 x 4096 x 5120 would
+    need two rounds of 64x32 tiles that lose to a split in five, so it
+    splits."""
     n = ctypes.c_size_t()
     for (M, N, K), b_kc, split in (((2048, 1536, 8960), False, True), ((2048, 1536, 8960), True, False),
                                    ((1024, 4096, 4096), True, False), ((2048, 256, 4096), True, False),
                                    ((1024, 256, 4096), True, False), ((2048, 256, 4096), False, True),
-                                   ((256, 4096, 4096), True, True)):
+                                   ((256, 4096, 4096), True, False), ((256, 4096, 5120), True, True)):
         sbk, sbn = (1, K) if b_kc else (N, 1)
         _lib.check(_lib.workspace_size(M, N, K, K, 1, sbk, sbn, 0, 0, ctypes.byref(n)))
         assert (n.value > 0) == split, (M, N, K, b_kc)

@@ -601,14 +601,14 @@ def _split_plan(ga, gb):
 
 @pytest.mark.parametrize("shape, b_layout", [((256, 256, 4096), "row-major"), ((1024, 256, 4096), "row-major"),
                                              ((300, 200, 4200), "row-major"), ((512, 384, 8960), "row-major"),
-                                             ((256, 4096, 4096), "w.t()")])
+                                             ((256, 4096, 5120), "w.t()")])
 def test_split_k_matches_oracle(shape, b_layout):
     """Shapes with few output tiles are split along K into chunk-aligned
     ranges; a second launch adds the FP32 partials per tile.  Results and
     flags match the oracle; repeated calls (sharing the stream's workspace)
     give identical bits.  (With b = w.t() most of these shapes take a K-group
-    tile instead: b is row-major there, except for a shape whose 64x32 grid
-    needs two rounds.)"""
+    tile instead: b is row-major there, except for a shape whose two rounds
+    of 64x32 tiles lose to a split in five.)"""
     M, N, K = shape
     a, w = rnd((M, K), 60 + K), rnd((N, K), 61 + K)
     ga, gb = a.cuda(), (w.cuda().t() if b_layout == "w.t()" else w.t().contiguous().cuda())
@@ -678,12 +678,12 @@ def test_split_k_overflow_in_every_wave_of_a_split_tile(tile, wm, wn):
 
 def test_split_k_bias_and_ws_entry_without_workspace():
     """A biased projection with few output tiles and long K (256 x 4096 x
-    4096) takes the split path through patch.linear and still equals the
+    5120) takes the split path through patch.linear and still equals the
     unfused y = mm(x2, w.t()); y += b bit for bit; f16acc_gemm_ws with no
     workspace is f16acc_gemm."""
     from f16acc_amd import _lib, patch
 
-    x, w, bias = rnd((256, 4096), 72).cuda(), rnd((4096, 4096), 73, 0.02).cuda(), rnd((4096,), 74, 0.02).cuda()
+    x, w, bias = rnd((256, 5120), 72).cuda(), rnd((4096, 5120), 73, 0.02).cuda(), rnd((4096,), 74, 0.02).cuda()
     assert _split_plan(x, w.t()) > 0
     unfused = f16acc.mm(x, w.t())
     unfused += bias
@@ -691,11 +691,11 @@ def test_split_k_bias_and_ws_entry_without_workspace():
         assert torch.equal(patch.linear(x, w, bias), unfused)
     c = torch.empty(256, 4096, device="cuda", dtype=torch.float16)
     st = torch.cuda.current_stream().cuda_stream
-    rc = _lib.gemm_ws(x.data_ptr(), w.data_ptr(), None, c.data_ptr(), None, 256, 4096, 4096, x.stride(0), 1,
-                      1, 4096, 4096, 1, 0, 1, st, None, 0)
+    rc = _lib.gemm_ws(x.data_ptr(), w.data_ptr(), None, c.data_ptr(), None, 256, 4096, 5120, x.stride(0), 1,
+                      1, 5120, 4096, 1, 0, 1, st, None, 0)
     assert rc == 0
     plain = torch.empty_like(c)
-    assert _lib.gemm(x.data_ptr(), w.data_ptr(), plain.data_ptr(), None, 256, 4096, 4096, x.stride(0), 1, 1, 4096,
+    assert _lib.gemm(x.data_ptr(), w.data_ptr(), plain.data_ptr(), None, 256, 4096, 5120, x.stride(0), 1, 1, 5120,
                      4096, 1, 0, 1, st) == 0
     assert torch.equal(c, plain)
     assert rel(c.cpu(), chunk32.mm(x.cpu(), w.cpu().t(), torch.float16, tile=(128, 128))) < TOL
