@@ -73,11 +73,12 @@ abi_version.restype = _int
 # Exported symbol names, as declared in include/f16acc.h.
 EXPORTS = ("f16acc_gemm", "f16acc_gemm_bias", "f16acc_gemm_ws", "f16acc_gemm_noalloc", "f16acc_workspace_size", "f16acc_gemm_tile", "f16acc_gemm_tile_ws", "f16acc_pack", "f16acc_tile_config", "f16acc_block_tile", "f16acc_strerror",
            "f16acc_abi_version", "f16acc_tail_split")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 OUT_F16, OUT_F32 = 0, 1
 E_ARG, E_UNSUPPORTED, E_SCRATCH, E_DEVICE = -1, -2, -3, -4
-TILES = ("256x256", "256x128", "128x256", "128x128", "generic", "64x64", "128x96k2", "64x32k4")  # F16ACC_TILE_* ids
+TILES = ("256x256", "256x128", "128x256", "128x128", "generic", "64x64", "128x96k2", "64x32k4",
+         "256x288")  # F16ACC_TILE_* ids
 TILE_GENERIC = 4
 
 if abi_version() != ABI_VERSION:

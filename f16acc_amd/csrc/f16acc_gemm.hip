@@ -177,10 +177,15 @@ struct Cfg {
   static constexpr int STAGE = A_STAGE + B_STAGE;
   static constexpr int RING = NS * STAGE;                        // one K group's LDS ring
   static constexpr int LA = BM * 8 / TG;                         // 16-byte units per thread per stage
-  static constexpr int LB = BN * 8 / TG;
+  static constexpr int LBF = BN * 8 / TG;                        // b units every thread copies
+  static constexpr int LB = (BN * 8 + TG - 1) / TG;              // ... plus a last, partial one
+  static constexpr int LB_WAVES = BN * 8 % TG / 64;              // waves that copy the partial unit
   static constexpr int UB = BN / 8;                              // NC: units per k-row
   static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave tile must be whole 16x16 blocks");
-  static_assert(BM * 8 % TG == 0 && BN * 8 % TG == 0, "stage must split evenly over a group's threads");
+  static_assert(BM * 8 % TG == 0, "A stage must split evenly over a group's threads");
+  // a K-contiguous b of BN rows may end in a unit that only the first
+  // LB_WAVES waves copy (256x288: 4.5 units a thread)
+  static_assert(BN * 8 % TG == 0 || (BL == kKC && BN * 8 % 64 == 0), "b stage must split over whole waves");
   // The NC swizzle spreads a k-row over 16 units; at BN = 64 (8 units) it
   // folds onto 8 (still a permutation, some transpose reads then conflict).
   // It needs a power of two of units per k-row.
@@ -195,6 +200,7 @@ struct Cfg {
   // inside the workgroup instead.
   static constexpr bool SPLITTABLE = FM * FN <= 16 && KG == 1;
   static_assert((NS - 2) * (LA + LB) <= 63, "outstanding loads must fit vmcnt");
+  static_assert(NS == 2 || LB == LBF, "a partial b unit needs the two-stage ring's vmcnt(0) waits");
 };
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -304,11 +310,12 @@ struct FastLoader {
     i32x4 ra, rb;  // unit-0 resources of the stage
     int va, vb;    // this lane's offsets for the stage
     int lds;
+    int wave;
     const FastLoader* ld;
     __device__ __forceinline__ void unit(int j) const {
       if (j < C::LA)
         lds_dma16(srd_at(ra, j * ld->a_step), lds + j * C::TG * 16, va);
-      else
+      else if (j < C::LA + C::LBF || wave < C::LB_WAVES)  // wave-uniform
         lds_dma16(srd_at(rb, (j - C::LA) * ld->b_step), lds + C::A_STAGE + (j - C::LA) * C::TG * 16, vb);
     }
     __device__ __forceinline__ void all() const {
@@ -335,6 +342,7 @@ struct FastLoader {
       st.vb = b_col;
     }
     st.lds = __builtin_amdgcn_readfirstlane((int)(uint32_t)(size_t)slot + wave * 64 * 16);
+    st.wave = wave;
     st.ld = this;
     return st;
   }
@@ -718,6 +726,7 @@ struct RegLoader {
   int b_row, b_k;  // unit 0 of B: KC tile column and first k; NC k-row and first column
 
   __device__ __forceinline__ void init(int tid) {
+    static_assert(C::LB == C::LBF, "every thread copies the same b units");
     a_row = tid >> 3;
     a_k = 8 * ((tid & 7) ^ kc_swz(a_row));
     if (C::BL == kKC) {
@@ -990,13 +999,19 @@ __device__ __forceinline__ void store_tile_staged(const Params& p, int64_t m0, i
 // element.
 typedef f32x4 __attribute__((aligned(4))) f32x4_a4;
 
+// The fewest passes, at least `least`, that split fn column blocks evenly.
+constexpr int passes(int fn, int least) {
+  int p = least < 1 ? 1 : least;
+  while (fn % p) ++p;
+  return p;
+}
+
 template <class C, int SMEM>
 __device__ __forceinline__ void store_tile_staged32(const Params& p, int64_t m0, int64_t n0, int wm, int wn,
                                                     int lane, int wave, char LDS_AS* smem,
                                                     const f32x4 (&acc)[C::FM][C::FN]) {
   constexpr int NW = C::WAVES_M * C::WAVES_N;
-  constexpr int P = (NW * C::WTM * C::WTN * 4 + SMEM - 1) / SMEM;
-  static_assert(C::FN % P == 0, "passes must split the wave tile's column blocks evenly");
+  constexpr int P = passes(C::FN, (NW * C::WTM * C::WTN * 4 + SMEM - 1) / SMEM);
   constexpr int PW = C::WTN / P;  // columns per pass
   constexpr int U = PW / 4;       // 16-byte units per staged row
   constexpr int ROW = PW * 4;
@@ -1204,7 +1219,11 @@ __device__ __forceinline__ int part_offset(int i, int j, int tid) {
 template <class C, int LD, bool CHUNKED, bool OUT32>
 __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) void gemm_kernel(Params p) {
   static_assert(C::KG == 1 || LD == kDma, "K groups run on the direct-to-LDS loader only");
-  constexpr int kSmem = LD == kGather ? C::STAGE : C::KG * C::RING;
+  // the rings, or the fp16 tile staged for its store where that is larger
+  // (256x288: 136 KiB of rings, 144 KiB of tile)
+  constexpr int kRings = C::KG * C::RING, kTileBytes = C::BM * C::BN * 2;
+  constexpr int kSmem = LD == kGather ? C::STAGE : kRings > kTileBytes ? kRings : kTileBytes;
+  static_assert(kSmem <= 160 * 1024 - 1024, "LDS of a CU");
   __shared__ __attribute__((aligned(1024))) char smem_raw[kSmem];
   __shared__ int tile_bad;
   char LDS_AS* smem = (char LDS_AS*)smem_raw;
@@ -1355,6 +1374,7 @@ __global__ __launch_bounds__(256) void pack_kernel(const f16* __restrict__ src, 
 //   5   64x64    4      32x32      2 x 16 KiB    4
 //   6   128x96   2 x 4  64x48      2 x 2 x 28 KiB  1   (two K groups)
 //   7   64x32    4 x 2  32x32      4 x 3 x 12 KiB  1   (four K groups)
+//   8   256x288  8      64x144     2 x 68 KiB    1   (K-contiguous b)
 template <int BL> using Cfg0 = Cfg<256, 256, 4, 2, 2, BL>;
 template <int BL> using Cfg1 = Cfg<256, 128, 4, 2, 3, BL>;
 template <int BL> using Cfg2 = Cfg<128, 256, 2, 4, 3, BL>;
@@ -1367,13 +1387,17 @@ using CfgG = Cfg<128, 128, 2, 2, 2, kKC>;
 // 32x32 with three-stage rings (144 KiB of LDS).
 using Cfg6 = Cfg<128, 96, 2, 2, 2, kKC, 2, 2>;
 using Cfg7 = Cfg<64, 32, 2, 1, 3, kKC, 2, 4>;
+// 256x288: 256x256 widened by a ninth column block per wave (64x144), so
+// that 2048 x 8960 is one round of 256 tiles (8 x 32) instead of 280 256x256
+// tiles; K-contiguous b only (288 columns are 36 units of a k-row).
+using Cfg8 = Cfg<256, 288, 4, 2, 2, kKC>;
 
 struct TileInfo {
   int bm, bn, threads, per_cu;
 };
 constexpr TileInfo kTiles[F16ACC_NUM_TILES] = {
     {256, 256, 512, 1}, {256, 128, 512, 1}, {128, 256, 512, 1}, {128, 128, 256, 2}, {128, 128, 256, 2},
-    {64, 64, 256, 4},   {128, 96, 512, 1},  {64, 32, 512, 1}};
+    {64, 64, 256, 4},   {128, 96, 512, 1},  {64, 32, 512, 1},   {256, 288, 512, 1}};
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -1466,11 +1490,23 @@ inline int64_t split_count(int64_t tiles, int64_t slots, int64_t nsteps) {
 // a full round's time (one tile per CU; measured on MI355X at K = 1536 and
 // 4096: 45.1 -> 62.5 us and 108.7 -> 148.2 us from 16 to 256 tiles, 126.7 us
 // at 192), since fewer busy CUs share the clock and the memory system.
-inline double rounds_256(int64_t n, int cus) {
-  const double full = 256.0 * 256.0 / kTileRate[F16ACC_TILE_256x256];
+inline double rounds_of(int64_t n, int cus, double full) {
   const int64_t r = n % cus;
   const double f = (double)r / cus;
   return (double)(n / cus) * full + (r ? full * (0.73 + 0.27 * f * f * f) : 0.0);
+}
+
+inline double rounds_256(int64_t n, int cus) {
+  return rounds_of(n, cus, 256.0 * 256.0 / kTileRate[F16ACC_TILE_256x256]);
+}
+
+// 256x288 (K-contiguous b): 256x256 with a ninth column block per wave, so a
+// tile costs its area at 256x256's rate.  It wins where its tiles fill the
+// rounds better: Qwen2.5-1.5B gate/up (2048 x 8960) is 256 tiles, one round,
+// against 280 256x256 tiles (a ragged second round, or a cut with a second
+// launch for the last 768 columns).
+inline double rounds_288(int64_t n, int cus) {
+  return rounds_of(n, cus, 256.0 * 288.0 / kTileRate[F16ACC_TILE_256x256]);
 }
 
 // K-group tiles (kc: the operands allow them, a K-contiguous b on the fast
@@ -1510,6 +1546,13 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
       best_t = est;
     }
   }
+  if (kc) {
+    const double est = rounds_288(cdiv(M, 256) * cdiv(N, 288), cus);
+    if (est < best_t * 0.999) {
+      best = F16ACC_TILE_256x288;
+      best_t = est;
+    }
+  }
   const TileInfo& t = kTiles[best];
   const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn), slots = (int64_t)cus * t.per_cu;
   // Small grids: only when some CUs would get no workgroup at all.  With one
@@ -1540,7 +1583,8 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
     const TileInfo& s = kTiles[F16ACC_TILE_64x64];
     const int64_t stiles = cdiv(M, s.bm) * cdiv(N, s.bn);
     double est_best = (double)t.bm * t.bn * t.per_cu / kTileRate[best];
-    const int64_t splits = best == F16ACC_TILE_256x256 ? 1 : split_count(tiles, slots, cdiv(K, kStageK));
+    const int64_t splits =
+        best == F16ACC_TILE_256x256 || best == F16ACC_TILE_256x288 ? 1 : split_count(tiles, slots, cdiv(K, kStageK));
     if (splits > 1) {
       const double est_split = (double)cdiv(tiles * splits, slots) * est_best / splits * kSplitCost;
       if (est_split < est_best) est_best = est_split;
@@ -1583,6 +1627,10 @@ inline bool plan_tail(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak,
   const int64_t tm = cdiv(M, t.bm), tn = cdiv(N, t.bn), tiles = tm * tn;
   const int64_t rounds = tiles / cus;
   if (rounds < 1 || tiles % cus == 0) return false;
+  // no cut where the table takes 256x288 for the whole problem
+  if (fast_layout(N, K, sam, sak, sbk, sbn, a, b, 256, 288) == kKC &&
+      choose_tile(M, N, K, cus, nullptr, true) == F16ACC_TILE_256x288)
+    return false;
   double whole = 0;
   // (the estimates leave the K-group tiles out: the cuts were measured
   // against the other tiles)
@@ -1629,6 +1677,7 @@ inline Choice choose(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, 
   // 64x64).
   if (id == F16ACC_TILE_128x96_K2 && bl != kKC) id = F16ACC_TILE_128x128;
   if (id == F16ACC_TILE_64x32_K4 && bl != kKC) id = F16ACC_TILE_64x64;
+  if (id == F16ACC_TILE_256x288 && bl != kKC) id = F16ACC_TILE_256x256;
   if (bl >= 0) return Choice{id, F16ACC_FAMILY_FAST, bl};
   // Operands the copies cannot read: the tiles with registers to spare
   // stage them through registers (kReg); the others gather elements.  The
@@ -1796,6 +1845,7 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
       case 5: return (int)launch_fast<Cfg5>(q, ch.blayout, out32, chunked, st);
       case 6: return (int)launch_cfg<Cfg6, kDma>(q, out32, chunked, st);
       case 7: return (int)launch_cfg<Cfg7, kDma>(q, out32, chunked, st);
+      case 8: return (int)launch_cfg<Cfg8, kDma>(q, out32, chunked, st);
       default: return (int)launch_cfg<CfgG, kGather>(q, out32, chunked, st);
     }
   };
@@ -1852,7 +1902,7 @@ int scratch_ptr(void** out) {
 
 extern "C" {
 
-int f16acc_abi_version(void) { return 5; }
+int f16acc_abi_version(void) { return 6; }
 
 const char* f16acc_strerror(int code) {
   if (code == 0) return "success";

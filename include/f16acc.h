@@ -38,7 +38,8 @@ extern "C" {
                                    workgroup; K-contiguous b (else runs as 128x128) */
 #define F16ACC_TILE_64x32_K4 7  /* four K groups of 2 waves of 32x32 splitting K inside the
                                    workgroup; K-contiguous b (else runs as 64x64) */
-#define F16ACC_NUM_TILES 8
+#define F16ACC_TILE_256x288 8    /* 8 waves of 64x144; K-contiguous b (else runs as 256x256) */
+#define F16ACC_NUM_TILES 9
 
 #define F16ACC_FAMILY_FAST 0    /* direct global -> LDS copies of 16-byte units */
 #define F16ACC_FAMILY_GENERIC 1 /* strided element gather through registers */

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(dll, name), name
     assert sorted(_lib.EXPORTS) == names
-    assert _lib.abi_version() == _lib.ABI_VERSION == 5
+    assert _lib.abi_version() == _lib.ABI_VERSION == 6
 
 
 def test_gemm_rejects_bad_arguments_before_launching():
@@ -118,7 +118,8 @@ class _Fake:
     (4096, 4096, 4096, (4096, 1), (1, 4096), "fast", "256x256"),   # w.t() (KC loader)
     (8192, 8192, 8192, (8192, 1), (8192, 1), "fast", "256x256"),
     (2048, 151936, 1536, (1536, 1), (1, 1536), "fast", "256x256"),  # lm_head
-    (2048, 8960, 1536, (1536, 1), (1, 1536), "fast", "128x128"),   # 280 256-tiles: ragged 2nd wave
+    (2048, 8960, 1536, (1536, 1), (1, 1536), "fast", "256x288"),   # Qwen gate/up: 256 tiles, one round (280 of 256x256)
+    (2048, 8960, 1536, (1536, 1), (8960, 1), "fast", "128x128"),   # row-major b: no 256x288; ragged 2nd round
     (1024, 11008, 4096, (4096, 1), (1, 4096), "fast", "256x256"),  # 172 256-tiles: one partial round beats 688 128-tiles
     (2048, 2048, 1536, (1536, 1), (1, 1536), "fast", "128x128"),   # 256 128-tiles: one per CU, no 64x64 (22.8 vs 24.1 us)
     (1024, 4096, 4096, (4096, 1), (1, 4096), "fast", "128x128"),   # one per CU: no K split either (51.4 vs 54.1 us)
@@ -151,7 +152,7 @@ def test_tile_table(M, N, K, sa, sb, fam, tile):
 
 
 @pytest.mark.parametrize("tile", ["256x256", "256x128", "128x256", "128x128", "generic", "64x64", "128x96k2",
-                                  "64x32k4"])
+                                  "64x32k4", "256x288"])
 def test_forced_tile_resolves(tile):
     bm, bn = (128, 128) if tile == "generic" else (int(tile.split("x")[0]), int(tile.split("x")[1].split("k")[0]))
     # w.t() (K-contiguous b): every tile as forced
@@ -159,9 +160,9 @@ def test_forced_tile_resolves(tile):
     assert cfg["tile"] == tile and (cfg["bm"], cfg["bn"]) == (bm, bn)
     assert cfg["family"] == ("generic" if tile == "generic" else "fast")
     # a row-major b: the K-group tiles run as 128x128 and 64x64 (their K
-    # groups read a K-contiguous b only)
+    # groups read a K-contiguous b only), 256x288 as 256x256
     cfg = tile_config(_Fake((4096, 1024), (1024, 1)), _Fake((1024, 2048), (2048, 1)), tile)
-    assert cfg["tile"] == {"128x96k2": "128x128", "64x32k4": "64x64"}.get(tile, tile)
+    assert cfg["tile"] == {"128x96k2": "128x128", "64x32k4": "64x64", "256x288": "256x256"}.get(tile, tile)
     # strided operands: mm packs them for a forced fast tile, so the tile holds
     cfg = tile_config(_Fake((300, 256), (512, 2)), _Fake((256, 200), (700, 3)), tile)
     assert cfg["tile"] == tile
@@ -233,25 +234,28 @@ def test_patch_enable_disable_and_cpu_fallback():
     assert set(f16acc.__all__) == {"mm", "enable", "disable", "calls"}
 
 
-@pytest.mark.parametrize("M,N,K,want", [
-    (2048, 8960, 1536, 8192),   # Qwen2.5-1.5B gate/up: 280 tiles of 256x256 on 256 CUs
-    (8192, 8960, 1536, 8192),   # 1120 tiles: four rounds plus 96
-    (2048, 8960, 8960, 8192),   # long K: the tail may split along K instead
-    (4096, 4096, 4096, 0),      # whole rounds
-    (2048, 151936, 1536, 0),    # lm_head: the ragged round is half full, a tail gains < 3 %
-    (2048, 1536, 1536, 0),      # under one round
-    (8960, 2048, 1536, -8192),  # tall: the row cut fills the first round, the column cut would not
-    (8960, 4096, 1536, -8192),  # only the row cut gains
-    (4096, 8960, 1536, 8192),   # only the column cut gains
-    (4096, 11008, 4096, 0),     # a 69%-full last round costs less than the cut (measured 404.8 against 419.5 us)
-    (4096, 18944, 3584, 0),
+@pytest.mark.parametrize("M,N,K,want,want_kc", [
+    (2048, 8960, 1536, 8192, 0),       # Qwen2.5-1.5B gate/up: 280 tiles of 256x256 on 256 CUs (256 of 256x288)
+    (8192, 8960, 1536, 8192, 0),       # 1120 tiles: four rounds plus 96 (four rounds of 256x288)
+    (2048, 8960, 8960, 8192, 0),       # long K: the tail may split along K instead
+    (4096, 4096, 4096, 0, 0),          # whole rounds
+    (2048, 151936, 1536, 0, 0),        # lm_head: the ragged round is half full, a tail gains < 3 %
+    (2048, 1536, 1536, 0, 0),          # under one round
+    (8960, 2048, 1536, -8192, -8192),  # tall: the row cut fills the first round, the column cut would not
+    (8960, 4096, 1536, -8192, -8192),  # only the row cut gains
+    (4096, 8960, 1536, 8192, 0),       # only the column cut gains (two rounds of 256x288)
+    (4096, 11008, 4096, 0, 0),         # a 69%-full last round costs less than the cut (404.8 against 419.5 us)
+    (4096, 18944, 3584, 0, 0),
 ])
-def test_ragged_round_tail_plan(M, N, K, want):
+def test_ragged_round_tail_plan(M, N, K, want, want_kc):
     """Where f16acc_gemm cuts a ragged last 256x256 round into a second launch
-    (no GPU here: the planner assumes 256 CUs)."""
+    (no GPU here: the planner assumes 256 CUs): with a row-major b, and with
+    b = w.t(), where 256x288 tiles fill the rounds instead on some shapes."""
     n = ctypes.c_int64(-1)
-    _lib.check(_lib.tail_split(M, N, K, K, 1, 1, K, 0, 0, ctypes.byref(n)))
+    _lib.check(_lib.tail_split(M, N, K, K, 1, N, 1, 0, 0, ctypes.byref(n)))
     assert n.value == want
+    _lib.check(_lib.tail_split(M, N, K, K, 1, 1, K, 0, 0, ctypes.byref(n)))
+    assert n.value == want_kc
     assert _lib.tail_split(-1, N, K, K, 1, 1, K, 0, 0, ctypes.byref(n)) == -1  # F16ACC_E_ARG
 
 

@@ -42,17 +42,18 @@ def oracle(a, b, out_dtype, cfg, chunked=True):
     return chunk32.mm(a, b, out_dtype, chunked=chunked, tile=(cfg["bm"], cfg["bn"]), return_flags=True)
 
 
-ALL_TILES = ["256x256", "256x128", "128x256", "128x128", "generic", "64x64", "128x96k2", "64x32k4"]
+ALL_TILES = ["256x256", "256x128", "128x256", "128x128", "generic", "64x64", "128x96k2", "64x32k4", "256x288"]
 
 
-# K-group tiles and the tile each runs as with a row-major b (their K groups
-# read a K-contiguous b only)
-K_GROUP_FALLBACK = {"128x96k2": "128x128", "64x32k4": "64x64"}
+# Tiles that read a K-contiguous b only (the K-group tiles; 256x288, whose
+# k-rows of 36 units do not fit the transpose-read swizzle), and the tile
+# each runs as with a row-major b
+KC_ONLY_FALLBACK = {"128x96k2": "128x128", "64x32k4": "64x64", "256x288": "256x256"}
 
 
 def forced_tile_runs_as(tile, b_row_major):
     """The tile a forced tile runs as."""
-    return K_GROUP_FALLBACK.get(tile, tile) if b_row_major else tile
+    return KC_ONLY_FALLBACK.get(tile, tile) if b_row_major else tile
 
 
 def tile_dims(tile):
@@ -289,7 +290,7 @@ def test_every_tile_stores_unaligned_rows_and_edges(tile):
 # Waves of each tile configuration (rows x columns of waves); wave (wm, wn)
 # owns the (bm / rows) x (bn / columns) sub-tile at (wm, wn) of its tile.
 WAVES = {"256x256": (4, 2), "256x128": (4, 2), "128x256": (2, 4), "128x128": (2, 2), "generic": (2, 2),
-         "64x64": (2, 2), "128x96k2": (2, 2), "64x32k4": (2, 1)}
+         "64x64": (2, 2), "128x96k2": (2, 2), "64x32k4": (2, 1), "256x288": (4, 2)}
 
 
 def _wave_cases(tiles):
@@ -322,8 +323,8 @@ def test_every_tile_redoes_overflow_in_every_wave(tile, wm, wn):
     b[:, c0:c0 + 10] = 0.0
     b[:32, c0:c0 + 10], b[32:64, c0:c0 + 10], b[64:96, c0:c0 + 10], b[96:, c0:c0 + 10] = 30.0, -30.0, 30.0, -30.0
     b[127, c0:c0 + 10] = -29.0
-    # b row-major, except for the K-group tiles, which read a K-contiguous b only
-    ga, gb = a.cuda(), (b.t().contiguous().cuda().t() if tile in K_GROUP_FALLBACK else b.cuda())
+    # b row-major, except for the tiles that read a K-contiguous b only
+    ga, gb = a.cuda(), (b.t().contiguous().cuda().t() if tile in KC_ONLY_FALLBACK else b.cuda())
     cfg = tile_config(ga, gb, tile)
     assert cfg["tile"] == tile
     c, flags = mm_flags(ga, gb, torch.float32, tile=tile)
@@ -717,15 +718,17 @@ def _tail_split(ga, gb):
 @pytest.mark.parametrize("b_layout", ["w.t()", "row-major"])
 def test_ragged_round_tail_split_equals_single_grid(out_dtype, b_layout):
     """Qwen2.5-1.5B gate/up (2048 x 8960 x 1536): 280 tiles of 256x256 for
-    256 CUs.  mm runs columns 0..8191 as one round of 256x256 tiles and the
-    last 768 as a second launch (B offset by 8192 columns: a row offset of
-    w, a column offset of a row-major [K, N]); every element is computed as
+    256 CUs.  With a row-major b, mm runs columns 0..8191 as one round of
+    256x256 tiles and the last 768 as a second launch (B offset by 8192
+    columns); with b = w.t() it runs one round of 256 tiles of 256x288 (the
+    last column of tiles 32 wide) and no cut.  Every element is computed as
     in the single grid mm_flags launches (bit for bit) and matches the
     oracle."""
     x, w = rnd((2048, 1536), 80), rnd((8960, 1536), 81, 0.05)
     gx = x.cuda()
     gb = w.cuda().t() if b_layout == "w.t()" else w.t().contiguous().cuda()
-    assert _tail_split(gx, gb) == 8192
+    assert _tail_split(gx, gb) == (0 if b_layout == "w.t()" else 8192)
+    assert tile_config(gx, gb)["tile"] == ("256x288" if b_layout == "w.t()" else "128x128")
     c = f16acc.mm(gx, gb, out_dtype)
     c1, flags = mm_flags(gx, gb, out_dtype)
     assert int(flags.sum()) == 0
@@ -744,20 +747,32 @@ def test_ragged_round_tail_split_redoes_overflow_in_both_launches():
         w[cols, :] = 0.0
         w[cols, 0:32], w[cols, 32:64], w[cols, 64:96], w[cols, 96:128] = 30.0, -30.0, 30.0, -30.0
         w[cols, 127] = -29.0
-    gx, gw = x.cuda(), w.cuda()
-    assert _tail_split(gx, gw.t()) == 8192
-    c = f16acc.mm(gx, gw.t(), torch.float32)
+    gx, gb = x.cuda(), w.t().contiguous().cuda()  # row-major b: the cut
+    assert _tail_split(gx, gb) == 8192
+    c = f16acc.mm(gx, gb, torch.float32)
     assert torch.all(c[100:110, 500:510] == 100.0) and torch.all(c[100:110, 8500:8510] == 100.0)
     assert rel(c.cpu(), chunk32.mm(x, w.t(), torch.float32, tile=(128, 128))) < TOL
 
 
 def test_ragged_round_tail_split_fused_bias():
     """The tail launch gets the bias from its first column on: the fused
-    result still equals the unfused y = mm(x2, w.t()); y += b bit for bit."""
-    from f16acc_amd import patch
+    result still equals the unfused y = mm(x2, b); y += bias bit for bit.
+    patch.linear's own layout (b = w.t()) runs the same projection as one
+    256x288 round, whose last column of tiles is 32 wide: the fused bias is
+    bit-equal there too."""
+    from f16acc_amd import _lib, patch
 
     x, w, bias = rnd((2048, 1536), 84).cuda(), rnd((8960, 1536), 85, 0.02).cuda(), rnd((8960,), 86, 0.5).cuda()
-    assert _tail_split(x, w.t()) == 8192
+    b_rm = w.t().contiguous()
+    assert _tail_split(x, b_rm) == 8192
+    unfused = f16acc.mm(x, b_rm)
+    unfused += bias
+    fused = torch.empty_like(unfused)
+    st = torch.cuda.current_stream().cuda_stream
+    assert _lib.gemm_bias(x.data_ptr(), b_rm.data_ptr(), bias.data_ptr(), fused.data_ptr(), None, 2048, 8960,
+                          1536, x.stride(0), 1, 8960, 1, 8960, 1, 0, 1, st) == 0
+    assert torch.equal(fused, unfused)
+    assert _tail_split(x, w.t()) == 0 and tile_config(x, w.t())["tile"] == "256x288"
     unfused = f16acc.mm(x, w.t())
     unfused += bias
     with torch.no_grad():
