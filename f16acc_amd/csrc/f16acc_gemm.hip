@@ -163,10 +163,17 @@ enum Loader { kGather = 0, kDma = 1, kReg = 2 };
 // a K split inside one workgroup: shapes with few tiles (Qwen2.5-1.5B k/v
 // and q/o at 2048 tokens) get more waves per tile and shorter K loops
 // without a second launch or a workspace.
-template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int NS_, int BL_, int WPE_ = 2, int KG_ = 1>
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int NS_, int BL_, int WPE_ = 2, int KG_ = 1, int NSL_ = 0>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, NS = NS_, BL = BL_;
   static constexpr int WPE = WPE_, KG = KG_;
+  // Split phases (NSL_ > 0, K groups only): the upper half of the K groups
+  // ("late" groups, whose waves are the second wave on each SIMD) multiply a
+  // stage first and copy two stages ahead at its end, out of phase with the
+  // lower half, which copy at a stage's start; late groups have NSL-stage
+  // rings.
+  static constexpr bool SPLIT = NSL_ > 0 && KG_ > 1;
+  static constexpr int NSL = SPLIT ? NSL_ : NS_;
   static constexpr int NWG = WAVES_M * WAVES_N;                 // waves per K group
   static constexpr int TG = 64 * NWG;                            // threads per K group
   static constexpr int T = TG * KG;                              // threads per workgroup
@@ -176,6 +183,8 @@ struct Cfg {
   static constexpr int B_STAGE = BN * kStageK * 2;
   static constexpr int STAGE = A_STAGE + B_STAGE;
   static constexpr int RING = NS * STAGE;                        // one K group's LDS ring
+  static constexpr int RING_L = NSL * STAGE;                     // ... a late group's
+  static constexpr int RINGS = SPLIT ? KG / 2 * (RING + RING_L) : KG * RING;  // all groups' rings
   static constexpr int LA = BM * 8 / TG;                         // 16-byte units per thread per stage
   static constexpr int LBF = BN * 8 / TG;                        // b units every thread copies
   static constexpr int LB = (BN * 8 + TG - 1) / TG;              // ... plus a last, partial one
@@ -190,17 +199,22 @@ struct Cfg {
   // folds onto 8 (still a permutation, some transpose reads then conflict).
   // It needs a power of two of units per k-row.
   static_assert(BL == kKC || (BN >= 64 && (UB & (UB - 1)) == 0), "NC k-rows need 2^n >= 8 units");
-  static_assert(NS >= 2 && KG * RING <= 160 * 1024, "LDS rings must fit the 160 KiB of a CU");
+  static_assert(NS >= 2 && NSL >= 2 && RINGS <= 160 * 1024, "LDS rings must fit the 160 KiB of a CU");
+  static_assert(!SPLIT || (KG % 2 == 0 && NSL >= 3), "late groups copy two stages ahead");
+  // byte offset of K group g's ring
+  static constexpr int ring_base(int g) {
+    return !SPLIT ? g * RING : g < KG / 2 ? g * RING : KG / 2 * RING + (g - KG / 2) * RING_L;
+  }
   static_assert(KG >= 1 && T <= 1024, "at most 1024 threads per workgroup");
   // the group reduction parks groups 1..KG-1's sums in the (free) rings
-  static_assert((KG - 1) * BM * BN * 4 <= KG * RING, "group sums must fit the LDS rings");
+  static_assert((KG - 1) * BM * BN * 4 <= RINGS, "group sums must fit the LDS rings");
   // Split-K partial stores are compiled only into tiles of 64x64 per wave:
   // at 64x128 per wave the chunked kernel already uses ~240 of its 256
   // registers, and the extra path would make it spill.  K-group tiles split
   // inside the workgroup instead.
   static constexpr bool SPLITTABLE = FM * FN <= 16 && KG == 1;
-  static_assert((NS - 2) * (LA + LB) <= 63, "outstanding loads must fit vmcnt");
-  static_assert(NS == 2 || LB == LBF, "a partial b unit needs the two-stage ring's vmcnt(0) waits");
+  static_assert((NSL - 2) * (LA + LB) <= 63 && (NS - 2) * (LA + LB) <= 63, "outstanding loads must fit vmcnt");
+  static_assert((NS == 2 && NSL == 2) || LB == LBF, "a partial b unit needs the two-stage ring's vmcnt(0) waits");
 };
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -472,7 +486,9 @@ __device__ __forceinline__ void pipe_drain(Pipe<C>& pp, int lane, f32x4 (&acc)[C
   }
 }
 
-template <class C, bool CHUNKED>
+// LATE: a late K group of a split-phase tile (Cfg::SPLIT) issues the copies
+// `next` after the stage's MFMAs instead of before them.
+template <class C, bool CHUNKED, bool LATE = false>
 __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, int wn, int lane,
                                               f32x4 (&acc)[C::FM][C::FN],
                                               const typename FastLoader<C>::Stage& next, bool has_next,
@@ -490,7 +506,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
     constexpr bool kSpread = C::FM * C::FN >= 32;
     constexpr int kDmaCols = kSpread ? (C::FN / 2 < kUnits ? C::FN / 2 : kUnits) : 1;
     constexpr int kPerCol = (kUnits + kDmaCols - 1) / kDmaCols;
-    if (!kSpread && has_next) next.all();
+    if (!LATE && !kSpread && has_next) next.all();
 #pragma unroll
     for (int i = 0; i < C::FM; ++i)
 #pragma unroll
@@ -515,6 +531,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b1, af[i][1], acc[i][j], 0, 0, 0);
       }
     }
+    if (LATE && has_next) next.all();
     return;
   }
   // Chunked: blocks t = 0 .. FM*FN-1 (i = t % FM fastest), software
@@ -547,7 +564,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
   constexpr int kUnits = C::LA + C::LB;
   constexpr bool kSpread = T >= 32;
   constexpr int kDmaEvery = T / (2 * kUnits) > 0 ? T / (2 * kUnits) : 1;
-  if (!kSpread && has_next) next.all();
+  if (!LATE && !kSpread && has_next) next.all();
   // Tiles of 4-wave workgroups run two or four workgroups per CU, so a
   // SIMD's waves belong to workgroups in different phases: raising the
   // priority of a wave in its MFMA loop over one in its barrier and copy
@@ -584,6 +601,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
     }
   }
   if (kPrio) __builtin_amdgcn_s_setprio(0);
+  if (LATE && has_next) next.all();
 }
 
 // Whole K loop of the fast path: an NS-stage LDS ring.  The copies of the
@@ -597,32 +615,40 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
 // groups of a workgroup share its barriers, so a group with fewer stages
 // than another keeps stepping, without work, until the longest is done.
 // `wave` is the wave's index inside its K group, smem that group's ring.
-template <class C, bool CHUNKED>
+//
+// LATE (the late K groups of a split-phase tile): NSL-stage ring, and the
+// copies of stage s + NSL - 1 go out after stage s is multiplied, into the
+// slot stage s - 1 used (its reads retired by this step's barrier).  The
+// two waves of a SIMD then overlap: while an early wave issues its copies
+// (the CU's address unit takes them one at a time), the late wave on the
+// same SIMD multiplies, and the other way round at the end of the stage.
+template <class C, bool CHUNKED, bool LATE = false>
 __device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t n0, int64_t kbeg, int64_t kend,
                                             char LDS_AS* smem, FastLoader<C>& ld, int wave, int wm, int wn, int lane,
                                             f32x4 (&acc)[C::FM][C::FN], int64_t iters = 0) {
+  constexpr int NSX = LATE ? C::NSL : C::NS;
   const int64_t nsteps = kend > kbeg ? (kend - kbeg + kStageK - 1) / kStageK : 0;
   if (iters < nsteps) iters = nsteps;
   if (iters <= 0) return;
 #pragma unroll
-  for (int s0 = 0; s0 < C::NS - 1; ++s0)
+  for (int s0 = 0; s0 < NSX - 1; ++s0)
     if (s0 < nsteps) ld.issue(p, m0, n0, kbeg + (int64_t)s0 * kStageK, kend, smem + s0 * C::STAGE, wave);
   int slot = 0;
   Pipe<C> pp;
   for (int64_t s = 0; s < iters; ++s) {
-    if (s + C::NS - 2 < nsteps)
-      wait_vm<(C::NS - 2) * (C::LA + C::LB)>();
+    if (s + NSX - 2 < nsteps)
+      wait_vm<(NSX - 2) * (C::LA + C::LB)>();
     else
       wait_vm0();
     __syncthreads();
     if (C::KG == 1 || s < nsteps) {
-      const int64_t nxt = s + C::NS - 1;
-      const int nslot = slot == 0 ? C::NS - 1 : slot - 1;  // (s + NS - 1) % NS
+      const int64_t nxt = s + NSX - 1;
+      const int nslot = slot == 0 ? NSX - 1 : slot - 1;  // (s + NSX - 1) % NSX
       const typename FastLoader<C>::Stage next =
           ld.stage(p, m0, n0, kbeg + nxt * kStageK, kend, smem + nslot * C::STAGE, wave);
-      compute_stage<C, CHUNKED>(smem + slot * C::STAGE, wm, wn, lane, acc, next, nxt < nsteps, pp);
+      compute_stage<C, CHUNKED, LATE>(smem + slot * C::STAGE, wm, wn, lane, acc, next, nxt < nsteps, pp);
     }
-    slot = slot + 1 == C::NS ? 0 : slot + 1;
+    slot = slot + 1 == NSX ? 0 : slot + 1;
   }
   if (CHUNKED && nsteps > 0) pipe_drain<C>(pp, lane, acc);
   __syncthreads();  // LDS free for a redo pass
@@ -699,7 +725,10 @@ __device__ __forceinline__ void k_groups_fast(const Params& p, int64_t m0, int64
                                               int LDS_AS* flag = nullptr) {
   int64_t gbeg = kbeg, gend = kend, iters = 0;
   if (C::KG > 1) iters = group_range<C>(kbeg, kend, g, &gbeg, &gend);
-  k_loop_fast<C, CHUNKED>(p, m0, n0, gbeg, gend, smem + g * C::RING, ld, lw, wm, wn, lane, acc, iters);
+  if (C::SPLIT && g >= C::KG / 2)  // wave-uniform
+    k_loop_fast<C, CHUNKED, true>(p, m0, n0, gbeg, gend, smem + C::ring_base(g), ld, lw, wm, wn, lane, acc, iters);
+  else
+    k_loop_fast<C, CHUNKED>(p, m0, n0, gbeg, gend, smem + C::ring_base(g), ld, lw, wm, wn, lane, acc, iters);
   group_reduce<C>(smem, g, ltid, acc, flag);
 }
 
@@ -1221,7 +1250,7 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) 
   static_assert(C::KG == 1 || LD == kDma, "K groups run on the direct-to-LDS loader only");
   // the rings, or the fp16 tile staged for its store where that is larger
   // (256x288: 136 KiB of rings, 144 KiB of tile)
-  constexpr int kRings = C::KG * C::RING, kTileBytes = C::BM * C::BN * 2;
+  constexpr int kRings = C::RINGS, kTileBytes = C::BM * C::BN * 2;
   constexpr int kSmem = LD == kGather ? C::STAGE : kRings > kTileBytes ? kRings : kTileBytes;
   static_assert(kSmem <= 160 * 1024 - 1024, "LDS of a CU");
   __shared__ __attribute__((aligned(1024))) char smem_raw[kSmem];
@@ -1372,8 +1401,8 @@ __global__ __launch_bounds__(256) void pack_kernel(const f16* __restrict__ src, 
 //   3   128x128  4      64x64      2 x 32 KiB    2
 //   4   128x128  4      64x64      1 x 32 KiB    generic strided gather path
 //   5   64x64    4      32x32      2 x 16 KiB    4
-//   6   128x96   2 x 4  64x48      2 x 2 x 28 KiB  1   (two K groups)
-//   7   64x32    4 x 2  32x32      4 x 3 x 12 KiB  1   (four K groups)
+//   6   128x96   2 x 4  64x48      (2 + 3) x 28 KiB  1   (two K groups, split phases)
+//   7   64x32    4 x 2  32x32      2 x (2 + 3) x 12 KiB  1   (four K groups, split phases)
 //   8   256x288  8      64x144     2 x 68 KiB    1   (K-contiguous b)
 template <int BL> using Cfg0 = Cfg<256, 256, 4, 2, 2, BL>;
 template <int BL> using Cfg1 = Cfg<256, 128, 4, 2, 3, BL>;
@@ -1383,10 +1412,13 @@ template <int BL> using Cfg5 = Cfg<64, 64, 2, 2, 2, BL, 4>;
 using CfgG = Cfg<128, 128, 2, 2, 2, kKC>;
 // K-group tiles, K-contiguous b only (a row-major b's k-rows of 12 or 4
 // units do not fit the transpose-read swizzle): 128x96 as two groups of 4
-// waves of 64x48 with two-stage rings, 64x32 as four groups of 2 waves of
-// 32x32 with three-stage rings (144 KiB of LDS).
-using Cfg6 = Cfg<128, 96, 2, 2, 2, kKC, 2, 2>;
-using Cfg7 = Cfg<64, 32, 2, 1, 3, kKC, 2, 4>;
+// waves of 64x48, 64x32 as four groups of 2 waves of 32x32; split phases,
+// the early groups on two-stage rings, the late ones on three (140 KiB and
+// 120 KiB of LDS).  Measured against one phase (two-stage rings on 128x96,
+// three-stage on 64x32): Qwen2.5-1.5B q/o 18.46 -> 18.26 us, down 80.8 ->
+// 80.0, k/v 7.67 -> 7.35 (per call, same bits).
+using Cfg6 = Cfg<128, 96, 2, 2, 2, kKC, 2, 2, 3>;
+using Cfg7 = Cfg<64, 32, 2, 1, 2, kKC, 2, 4, 3>;
 // 256x288: 256x256 widened by a ninth column block per wave (64x144), so
 // that 2048 x 8960 is one round of 256 tiles (8 x 32) instead of 280 256x256
 // tiles; K-contiguous b only (288 columns are 36 units of a k-row).
