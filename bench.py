@@ -20,7 +20,9 @@ redo.  Prints one JSON line:
 Other workloads (--workload) are sweeps for the design record, not bench lines;
 --workload shapes reports every configured shape against hipBLASLt;
 --workload redo_overhead times the shipped kernels against a build without the
-overflow flag and redo on data that never overflows;
+overflow flag and redo on data that never overflows; --workload
+overflow_split_redo times the overflow stress workload against a build that
+redoes flagged tiles in a split-K pass instead of in the same workgroup;
 --workload table_check times the per-shape table against every forced tile on
 llama-2-7B, llama-3-8B and Qwen2.5-7B layer shapes; --tile-calls runs every tile
 untimed for rocprofv3 counter passes.
@@ -437,10 +439,76 @@ def overflow_bench(steps, warmup):
     print(json.dumps(line), flush=True)
 
 
+def overflow_split_redo(rounds=5):
+    """The overflow stress workload on the shipped library (each flagged
+    tile redone in FP32 by its own workgroup, a straggler on its CU) against
+    libf16acc_amd_splitredo.so (-DF16ACC_SPLIT_REDO=1: the chunked launch
+    only flags; flagged tiles are recomputed in FP32 as 128x128 tiles split
+    three ways along K, plus a finishing launch; loaded here only), both on
+    the stress data and on its no-overflow twin, through f16acc_gemm with
+    the same inputs, timed in interleaved settled bursts (median over
+    rounds).  Checks: the same flags; unflagged tiles bit-equal; flagged
+    tiles against the FP32-accumulate mode (a different FP32 summation
+    order: the three K ranges are summed after)."""
+    import ctypes
+
+    from f16acc_amd import _lib, build
+    from f16acc_amd.kernel import mm_tile, tile_config
+
+    split = ctypes.CDLL(build.LIB_SPLITREDO)
+    g_split = split.f16acc_gemm
+    g_split.argtypes, g_split.restype = _lib.gemm.argtypes, _lib.gemm.restype
+    a_cpu, b_cpu, rows, cols = overflow_inputs()
+    data = {"overflow": (a_cpu.cuda(), b_cpu.cuda())}
+    _, _, ca, cb = make_inputs(a_cpu.shape[0], b_cpu.shape[1], a_cpu.shape[1], "row")
+    data["clean"] = (ca, cb)
+    st = torch.cuda.current_stream().cuda_stream
+    out = {}
+    times = {}
+    for dname, (a, b) in data.items():
+        M, K = a.shape
+        N = b.shape[1]
+        cfg = tile_config(a, b)
+        for lname, fn in (("shipped", _lib.gemm), ("split_redo", g_split)):
+            c = torch.empty(M, N, device="cuda", dtype=torch.float32)
+            fl = torch.zeros(cfg["tiles_m"] * cfg["tiles_n"], device="cuda", dtype=torch.uint8)
+
+            def call(c=c, fl=None, fn=fn, a=a, b=b):
+                _lib.check(fn(a.data_ptr(), b.data_ptr(), c.data_ptr(), fl, M, N, K, a.stride(0), a.stride(1),
+                              b.stride(0), b.stride(1), c.stride(0), c.stride(1), _lib.OUT_F32, 1, st))
+
+            call(fl=fl.data_ptr())
+            torch.cuda.synchronize()
+            out[(dname, lname)] = (c.clone(), fl.clone())
+            times[(dname, lname)] = (call, [])
+    for _ in range(rounds):  # interleaved, so clock drift falls on all alike
+        for key, (call, ts) in times.items():
+            ts.append(settled_time(call))
+    a, b = data["overflow"]
+    cfg = tile_config(a, b)
+    (c_ship, f_ship), (c_split, f_split) = out[("overflow", "shipped")], out[("overflow", "split_redo")]
+    c32 = mm_tile(a, b, cfg["tile"], torch.float32, chunked=False)
+    bm, bn = cfg["bm"], cfg["bn"]
+    M, N = c_ship.shape
+    mask = f_ship.view(cfg["tiles_m"], cfg["tiles_n"]).bool().repeat_interleave(bm, 0).repeat_interleave(bn, 1)[:M, :N]
+    ref = c32[mask].double()
+    us = {f"{d}_{l}_us": round(statistics.median(ts) * 1e6, 2) for (d, l), (_, ts) in times.items()}
+    line = {"workload": "overflow stress 4096^3, fp32 out, B row-major: in-kernel redo vs split redo",
+            "tile": cfg["tile"], "flagged_tiles": int(f_ship.sum()), "same_flags": bool(torch.equal(f_ship, f_split)),
+            **us,
+            "overflow_cost_shipped_pct": round((us["overflow_shipped_us"] / us["clean_shipped_us"] - 1) * 100, 1),
+            "overflow_cost_split_pct": round((us["overflow_split_redo_us"] / us["clean_shipped_us"] - 1) * 100, 1),
+            "split_redo_clean_cost_pct": round((us["clean_split_redo_us"] / us["clean_shipped_us"] - 1) * 100, 1),
+            "unflagged_bit_equal": bool(torch.equal(c_ship[~mask], c_split[~mask])),
+            "shipped_redone_equal_fp32_mode": bool(torch.equal(c_ship[mask], c32[mask])),
+            "split_redone_max_rel_diff_vs_fp32_mode": ((c_split[mask].double() - ref).abs().max() / ref.abs().max()).item(),
+            "clean_outputs_bit_equal": bool(torch.equal(out[("clean", "shipped")][0], out[("clean", "split_redo")][0]))}
+    print(json.dumps(line), flush=True)
+
+
 # Shapes of the redo-overhead A/B: the overflow stress config's no-overflow
 # twin (4096^3, A and B ~ N(0, 1), fp32 out), the 8192^3 square GEMM and the
-# Qwen2.5-1.5B layers at 2048 tokens (64x64 tiles, split-K with its finishing
-# launch, the ragged-round second launch).
+# Qwen2.5-1.5B layers at 2048 tokens (the K-group tiles, 256x288).
 REDO_SHAPES = (("gemm4096_f32", 4096, 4096, 4096, "row", torch.float32),
                ("gemm8192", 8192, 8192, 8192, "row", torch.float16),
                ("qwen_qo", 2048, 1536, 1536, "t", torch.float16),
@@ -594,7 +662,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="gemm4096",
-                    choices=sorted(WORKLOADS) + ["copy", "overflow", "qwen2_prefill", "redo_overhead", "shapes",
+                    choices=sorted(WORKLOADS) + ["copy", "overflow", "overflow_split_redo", "qwen2_prefill",
+                                                 "redo_overhead", "shapes",
                                                  "table_check"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and oracle comparison")
     ap.add_argument("--preheat", type=float, default=PREHEAT_S,
@@ -620,6 +689,8 @@ def main():
         return shapes_report(list(WORKLOADS))
     if args.workload == "overflow":
         return overflow_bench(args.steps, args.warmup)
+    if args.workload == "overflow_split_redo":
+        return overflow_split_redo()
     if args.workload == "redo_overhead":
         return redo_overhead()
     if args.workload == "qwen2_prefill":

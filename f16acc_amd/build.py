@@ -22,6 +22,9 @@ LIB = os.path.join(OUT_DIR, "libf16acc_amd.so")
 # The same source with the tile flag and FP32 redo compiled out
 # (-DF16ACC_NO_REDO=1): only bench.py's redo-overhead A/B loads it.
 LIB_NOREDO = os.path.join(OUT_DIR, "libf16acc_amd_noredo.so")
+# ... and with the split redo in place of the in-kernel one for 256x256
+# (-DF16ACC_SPLIT_REDO=1): only bench.py's overflow workload loads it.
+LIB_SPLITREDO = os.path.join(OUT_DIR, "libf16acc_amd_splitredo.so")
 CHUNKRATE = os.path.join(OUT_DIR, "chunkrate")  # MFMA / chunk-epilogue microbenchmark
 ARCH = "gfx950"
 
@@ -68,9 +71,10 @@ def _finish(job, verbose):
 
 
 def build(verbose=False):
-    """Compile the library, its no-redo twin and the chunkrate
-    microbenchmark (three hipcc processes at once)."""
+    """Compile the library, its no-redo and split-redo twins and the
+    chunkrate microbenchmark (four hipcc processes at once)."""
     jobs = [_start(HIP_FLAGS, SRC, LIB), _start(HIP_FLAGS + ["-DF16ACC_NO_REDO=1"], SRC, LIB_NOREDO),
+            _start(HIP_FLAGS + ["-DF16ACC_SPLIT_REDO=1"], SRC, LIB_SPLITREDO),
             _start(COMMON_FLAGS, CHUNKRATE_SRC, CHUNKRATE)]
     errors = []
     for job in jobs:
