@@ -1660,13 +1660,14 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
 }
 
 // Ragged last round on the 256x256 tile.  When a shape's 256x256 tiles fill
-// some whole rounds of the CUs plus a few more (Qwen2.5-1.5B gate/up,
-// 2048x8960: 280 tiles on 256 CUs), the table would otherwise fall back to a
-// smaller tile everywhere, or run a second 256x256 round on a tenth of the
-// GPU.  Instead the problem is cut at a tile boundary: the first `at`
-// columns (or rows, for tall problems) as whole rounds of 256x256 tiles, the
-// rest as a second GEMM with the table's own choice for that narrower shape
-// (64x64 there: four times the tiles of 128x128 fill the GPU).  Both are
+// some whole rounds of the CUs plus a few more (2048x8960 with a row-major
+// b: 280 tiles on 256 CUs; with a K-contiguous b the table takes 256x288
+// there instead), the table would otherwise fall back to a smaller tile
+// everywhere, or run a second 256x256 round on a tenth of the GPU.  Instead
+// the problem is cut at a tile boundary: the first `at` columns (or rows,
+// for tall problems) as whole rounds of 256x256 tiles, the rest as a second
+// GEMM with the table's own choice for that narrower shape (64x64 there:
+// four times the tiles of 128x128 fill the GPU).  Both are
 // ordinary whole-K launches on the same stream, so every output element is
 // computed exactly as in a single launch; only the tile each element's
 // overflow redo covers differs, which the reference leaves to its autotuner

@@ -113,8 +113,8 @@ def test_qwen_layer_shapes_match_oracle(layer, n_out, n_in, biased):
     """Qwen2.5-1.5B's linear layers at 2048 tokens: x ~ N(0, 1), weight
     N(0, 0.02) stored [out, in] and multiplied as w.t(), q/k/v with an
     N(0, 0.02) bias.  mm matches the oracle with no tile flagged, through
-    whatever the shape plans (64x64 tiles, split-K for down, the ragged-round
-    second launch for gate/up); the fused bias equals the unfused
+    whatever the shape plans (the K-group tiles for q/o, k/v and down,
+    256x288 for gate/up, 256x256 for the lm_head); the fused bias equals the unfused
     `y = mm(x, w.t()); y += b` (f16acc/patch.py:28-30) bit for bit, and the
     patched nn.Linear returns those bits."""
     M = 2048
