@@ -265,6 +265,28 @@ def test_every_tile_matches_oracle(tile, K):
         assert rel(c32.cpu(), (a.float() @ b.float()).double()) < 1e-5
 
 
+@pytest.mark.parametrize("tile", ["256x256", "256x288", "128x96k2", "64x32k4"])
+def test_k_contiguous_slices_of_wider_buffers(tile):
+    """a = x[:, :K] of a wider [M, K + 64] buffer and b = w[:, :K].t() of a
+    wider [N, K + 40] weight: 16-byte aligned rows whose stride exceeds K,
+    which the direct-to-LDS copies read in place (the copies clip at K by
+    each stage's range and at M, N by the buffers' record counts).  Ragged
+    M, N, a partial last stage (K = 200), both output dtypes, values and
+    flags against the oracle."""
+    M, N, K = 300, 333, 200
+    xa, wb = rnd((M, K + 64), 130), rnd((N, K + 40), 131)
+    gxa, gwb = xa.cuda(), wb.cuda()
+    ga, gb = gxa[:, :K], gwb[:, :K].t()
+    assert ga.stride() == (K + 64, 1) and gb.stride() == (1, K + 40)
+    cfg = tile_config(ga, gb, tile)
+    assert cfg["tile"] == tile and cfg["family"] == "fast"
+    for out_dtype in (torch.float32, torch.float16):
+        c, flags = mm_flags(ga, gb, out_dtype, tile=tile)
+        ref, rflags = oracle(xa[:, :K], wb[:, :K].t(), out_dtype, cfg)
+        assert torch.equal(flags.cpu(), rflags)
+        assert rel(c.cpu(), ref) < TOL, (tile, out_dtype)
+
+
 @pytest.mark.parametrize("tile", ALL_TILES)
 def test_every_tile_stores_unaligned_rows_and_edges(tile):
     """fp16 rows of N = 517 halves start off 16-byte alignment, and M, N leave
