@@ -598,6 +598,52 @@ def test_fused_bias_equals_unfused_add_bit_for_bit(shape):
     assert torch.equal(fused, unfused)
 
 
+@pytest.mark.parametrize("M, N, K, tile", [(2048, 8192, 1536, "256x256"), (2048, 8960, 1536, "256x288"),
+                                           (2048, 1536, 1536, "128x96k2"), (2048, 256, 1536, "64x32k4"),
+                                           (256, 4096, 5120, "128x128")])
+def test_fused_bias_on_tiles_the_redo_recomputes(M, N, K, tile):
+    """The fused bias where the overflow redo stores a tile a second time:
+    the overflow closed form (reference tests/test_f16acc.py:91-101: chunk
+    partials of +-96000, exact sum 100) in 8 x 8 blocks at the four corner
+    tiles of each table pick (the last: 128x128 split along K).  The fused
+    result equals the reference's unfused y = mm(x2, w.t()); y += b
+    (f16acc/patch.py:28-30) bit for bit, in fp16 through the patched
+    nn.Linear and in fp32 through mm_bias; the redone blocks hold exactly
+    100 + b; exactly the four corner tiles are flagged."""
+    from f16acc_amd import patch
+    from f16acc_amd.kernel import mm_bias
+
+    x, w, bias = rnd((M, K), 90), rnd((N, K), 91, 0.02), rnd((N,), 92, 0.5)
+    pattern = torch.full((K,), 30.0)
+    pattern.view(-1, 32)[1::2] = -30.0
+    pattern[K - 1] = -29.0
+    rows, cols = [(5, 13), (M - 13, M - 5)], [(7, 15), (N - 11, N - 3)]
+    for r0, r1 in rows:
+        x[r0:r1] = 100.0
+    for c0, c1 in cols:
+        w[c0:c1] = pattern.half()
+    gx, gw, gbias = x.cuda(), w.cuda(), bias.cuda()
+    cfg = tile_config(gx, gw.t())
+    assert cfg["tile"] == tile
+    _, flags = mm_flags(gx, gw.t())
+    want = torch.zeros(cfg["tiles_m"], cfg["tiles_n"], dtype=torch.uint8)
+    want[0, 0] = want[0, -1] = want[-1, 0] = want[-1, -1] = 1
+    assert torch.equal(flags.cpu(), want)
+    unfused = f16acc.mm(gx, gw.t())
+    unfused += gbias
+    with torch.no_grad():
+        fused = patch.linear(gx, gw, gbias)
+    assert torch.equal(fused, unfused)
+    fused32 = mm_bias(gx, gw.t(), gbias, torch.float32)
+    unfused32 = f16acc.mm(gx, gw.t(), torch.float32) + gbias.float()
+    assert torch.equal(fused32, unfused32)
+    for r0, r1 in rows:
+        for c0, c1 in cols:
+            exact = (torch.full((c1 - c0,), 100.0, dtype=torch.float16) + bias[c0:c1]).expand(r1 - r0, -1)
+            assert torch.equal(fused[r0:r1, c0:c1].cpu(), exact)
+            assert torch.equal(fused32[r0:r1, c0:c1].cpu(), (100.0 + bias[c0:c1].float()).expand(r1 - r0, -1))
+
+
 def test_fused_bias_fp32_output_matches_oracle():
     from f16acc_amd.kernel import mm_bias
 
