@@ -45,7 +45,9 @@ PEAK_TFLOPS = 2516.6  # MI355X dense fp16 MFMA: 256 CU x 2.4 GHz x 4096 flop/clk
 METRIC = "TFLOPS at 4096³ fp16 GEMM (1 GPU, % of fp16 MFMA peak); max rel err vs FP64"
 REF_TFLOPS = 65.7  # reference README.md:29, RTX 4060 Ti, same GEMM (fp16 out)
 PREHEAT_S = 0.2  # seconds of back-to-back calls before the warm-up steps
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_4096_fp16out_rowmajorB_traffic.txt")
+# rocprofv3 HBM-counter summaries of the workloads that have one
+TRAFFIC_PROFILES = {w: os.path.join(ROOT, "profiles", f"{f}_fp16out_rowmajorB_traffic.txt")
+                    for w, f in (("gemm4096", "gemm_4096"), ("gemm8192", "gemm_8192"))}
 
 WORKLOADS = {
     # name: (M, N, K, b_layout, out_dtype)
@@ -117,10 +119,13 @@ def time_steps(op, steps, warmup):
     return wall, start.elapsed_time(stop) / 1e3
 
 
-def read_traffic():
-    """HBM bytes per launch from the committed rocprofv3 counter summary."""
+def read_traffic(workload):
+    """HBM bytes per launch from the workload's committed rocprofv3 counter
+    summary (None for a workload without one)."""
+    if workload not in TRAFFIC_PROFILES:
+        return None
     try:
-        with open(TRAFFIC_PROFILE) as f:
+        with open(TRAFFIC_PROFILES[workload]) as f:
             m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read(), re.M)
         return float(m.group(1)) if m else None
     except OSError:
@@ -746,7 +751,7 @@ def main():
         "frac_of_peak": round(value / PEAK_TFLOPS, 4),
         "max_rel_err_vs_fp64": err_fp64,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": read_traffic(),
+                     "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": read_traffic(args.workload),
                      "kernel_us": round(kernel_s * 1e6, 2)},
         "hipblaslt": {"value": round(flops / blas_t / 1e12, 2), "unit": "TFLOPS",
                       "op": "torch.mm (hipBLASLt), same inputs", "us": round(blas_t * 1e6, 2)},
