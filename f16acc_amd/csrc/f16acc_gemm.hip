@@ -515,6 +515,13 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
   const char LDS_AS* as = stage;
   const char LDS_AS* bs = stage + C::A_STAGE;
   const int r16 = lane & 15, g = lane >> 4;
+  // Copies spread over the stage go out without a test of has_next where b
+  // is K-contiguous: past the K range every unit reads zeros (offset kOob)
+  // into the slot the next stage would fill, which no wave reads again, and
+  // the stage stays one basic block (same bits; measured 1-2 % faster on
+  // 256x256 and 256x288, none with a row-major b).  The K loop waits for
+  // these copies before it hands the LDS on.
+  const bool spread_copy = C::BL == kKC || has_next;
   f16x8 af[C::FM][2];
   if (!CHUNKED) {
     // B one column ahead of its MFMAs; on 8-wave tiles the next stage's
@@ -538,7 +545,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
         bn0 = read_b<C>(bs, wn, j + 1, 0, lane);
         bn1 = read_b<C>(bs, wn, j + 1, 1, lane);
       }
-      if (kSpread && has_next && j < kDmaCols) {
+      if (kSpread && spread_copy && j < kDmaCols) {
 #pragma unroll
         for (int u = 0; u < kPerCol; ++u)
           if (j * kPerCol + u < kUnits) next.unit(j * kPerCol + u);
@@ -594,7 +601,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const int i = t % C::FM, j = t / C::FM;
-    if (kSpread && has_next && t % kDmaEvery == 0 && t / kDmaEvery < kUnits) next.unit(t / kDmaEvery);
+    if (kSpread && spread_copy && t % kDmaEvery == 0 && t / kDmaEvery < kUnits) next.unit(t / kDmaEvery);
     if (j == 0 && i + 1 < C::FM) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) af[i + 1][c] = read_kc<C>(as, wm * C::WTM + 16 * (i + 1) + r16, 4 * c + g);
@@ -670,7 +677,8 @@ __device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t
     slot = slot + 1 == NSX ? 0 : slot + 1;
   }
   if (CHUNKED && nsteps > 0) pipe_drain<C>(pp, lane, acc);
-  __syncthreads();  // LDS free for a redo pass
+  wait_vm0();       // copies past the K range (compute_stage) landed
+  __syncthreads();  // LDS free for the store's staging or a redo pass
 }
 
 // K range of K group g: the workgroup's range [kbeg, kend) in whole stages,
