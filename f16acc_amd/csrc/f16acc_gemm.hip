@@ -255,10 +255,20 @@ __device__ __forceinline__ i32x4 make_srd(const void* base) {
 // treat it as a store to every LDS buffer and wait for it before unrelated
 // ds_reads; the loop waits for it explicitly (wait_vm0 + barrier) before the
 // stage it fills is read.  M0 carries the LDS address; one wait state is
-// required between writing M0 and the DMA that reads it.
+// required between writing M0 and the DMA that reads it.  The resource is
+// wave-uniform by construction; PIN (a K-contiguous b, whose stage copies go
+// out with no branch around them) pins it to scalar registers with
+// readfirstlane, where the compiler would otherwise keep a copy in vector
+// registers.  A row-major b's loop keeps the code it was measured with.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved: the asm sets it itself
-__device__ __forceinline__ void lds_dma16(const i32x4& srd, int lds, int voff) {
+template <bool PIN>
+__device__ __forceinline__ void lds_dma16(const i32x4& rsrc, int lds, int voff) {
+  i32x4 srd = rsrc;
+  if constexpr (PIN) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) srd[k] = __builtin_amdgcn_readfirstlane(rsrc[k]);
+  }
   asm volatile(
       "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
@@ -346,14 +356,19 @@ struct FastLoader {
     int wave;
     const FastLoader* ld;
     __device__ __forceinline__ void unit(int j) const {
+      constexpr bool kPin = C::BL == kKC;
       if (j < C::LA)
-        lds_dma16(srd_at(ra, j * ld->a_step), lds + j * C::TG * 16, va);
+        lds_dma16<kPin>(srd_at(ra, j * ld->a_step), lds + j * C::TG * 16, va);
       else if (j < C::LA + C::LBF || wave < C::LB_WAVES)  // wave-uniform
-        lds_dma16(srd_at(rb, (j - C::LA) * ld->b_step), lds + C::A_STAGE + (j - C::LA) * C::TG * 16, vb);
+        lds_dma16<kPin>(srd_at(rb, (j - C::LA) * ld->b_step), lds + C::A_STAGE + (j - C::LA) * C::TG * 16, vb);
     }
     __device__ __forceinline__ void all() const {
 #pragma unroll
-      for (int j = 0; j < C::LA + C::LB; ++j) unit(j);
+      for (int j = 0; j < C::LA + C::LB; ++j) {
+        unit(j);
+        // K-contiguous b: each unit's resource computed next to its copy
+        if constexpr (C::BL == kKC) __builtin_amdgcn_sched_barrier(0);
+      }
     }
   };
 
@@ -506,8 +521,11 @@ __device__ __forceinline__ void pipe_drain(Pipe<C>& pp, int lane, f32x4 (&acc)[C
 }
 
 // LATE: a late K group of a split-phase tile (Cfg::SPLIT) issues the copies
-// `next` after the stage's MFMAs instead of before them.
-template <class C, bool CHUNKED, bool LATE = false>
+// `next` after the stage's MFMAs instead of before them.  DMA: `next` is a
+// real stage of the direct-to-LDS loader (k_loop_fast); the register-staged
+// and gather loops pass an empty one with has_next false, and no copy may
+// go out.
+template <class C, bool CHUNKED, bool LATE = false, bool DMA = false>
 __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, int wn, int lane,
                                               f32x4 (&acc)[C::FM][C::FN],
                                               const typename FastLoader<C>::Stage& next, bool has_next,
@@ -515,13 +533,15 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
   const char LDS_AS* as = stage;
   const char LDS_AS* bs = stage + C::A_STAGE;
   const int r16 = lane & 15, g = lane >> 4;
-  // Copies spread over the stage go out without a test of has_next where b
-  // is K-contiguous: past the K range every unit reads zeros (offset kOob)
-  // into the slot the next stage would fill, which no wave reads again, and
-  // the stage stays one basic block (same bits; measured 1-2 % faster on
-  // 256x256 and 256x288, none with a row-major b).  The K loop waits for
-  // these copies before it hands the LDS on.
-  const bool spread_copy = C::BL == kKC || has_next;
+  // In the direct-to-LDS loop (DMA), the next stage's copies go out without
+  // a test of has_next where b is K-contiguous (except in a late K group):
+  // past the K range every unit reads zeros (offset kOob) into the slot the
+  // next stage would fill, which no wave reads again, and the stage stays
+  // one basic block (same bits; measured 1-2 % faster on 256x256 and
+  // 256x288, 6 % on 64x64, 0.2-1 % on the K-group tiles' early groups; none
+  // with a row-major b, and slower in the late groups).  The K loop waits
+  // for these copies before it hands the LDS on.
+  const bool copy_next = has_next || (DMA && C::BL == kKC);
   f16x8 af[C::FM][2];
   if (!CHUNKED) {
     // B one column ahead of its MFMAs; on 8-wave tiles the next stage's
@@ -532,7 +552,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
     constexpr bool kSpread = C::FM * C::FN >= 32;
     constexpr int kDmaCols = kSpread ? (C::FN / 2 < kUnits ? C::FN / 2 : kUnits) : 1;
     constexpr int kPerCol = (kUnits + kDmaCols - 1) / kDmaCols;
-    if (!LATE && !kSpread && has_next) next.all();
+    if (!LATE && !kSpread && copy_next) next.all();
 #pragma unroll
     for (int i = 0; i < C::FM; ++i)
 #pragma unroll
@@ -545,7 +565,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
         bn0 = read_b<C>(bs, wn, j + 1, 0, lane);
         bn1 = read_b<C>(bs, wn, j + 1, 1, lane);
       }
-      if (kSpread && spread_copy && j < kDmaCols) {
+      if (kSpread && copy_next && j < kDmaCols) {
 #pragma unroll
         for (int u = 0; u < kPerCol; ++u)
           if (j * kPerCol + u < kUnits) next.unit(j * kPerCol + u);
@@ -590,7 +610,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
   constexpr int kUnits = C::LA + C::LB;
   constexpr bool kSpread = T >= 32;
   constexpr int kDmaEvery = T / (2 * kUnits) > 0 ? T / (2 * kUnits) : 1;
-  if (!LATE && !kSpread && has_next) next.all();
+  if (!LATE && !kSpread && copy_next) next.all();
   // Tiles of 4-wave workgroups run two or four workgroups per CU, so a
   // SIMD's waves belong to workgroups in different phases: raising the
   // priority of a wave in its MFMA loop over one in its barrier and copy
@@ -601,7 +621,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const int i = t % C::FM, j = t / C::FM;
-    if (kSpread && spread_copy && t % kDmaEvery == 0 && t / kDmaEvery < kUnits) next.unit(t / kDmaEvery);
+    if (kSpread && copy_next && t % kDmaEvery == 0 && t / kDmaEvery < kUnits) next.unit(t / kDmaEvery);
     if (j == 0 && i + 1 < C::FM) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) af[i + 1][c] = read_kc<C>(as, wm * C::WTM + 16 * (i + 1) + r16, 4 * c + g);
@@ -672,7 +692,7 @@ __device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t
       const int nslot = slot == 0 ? NSX - 1 : slot - 1;  // (s + NSX - 1) % NSX
       const typename FastLoader<C>::Stage next =
           ld.stage(p, m0, n0, kbeg + nxt * kStageK, kend, smem + nslot * C::STAGE, wave);
-      compute_stage<C, CHUNKED, LATE>(smem + slot * C::STAGE, wm, wn, lane, acc, next, nxt < nsteps, pp);
+      compute_stage<C, CHUNKED, LATE, true>(smem + slot * C::STAGE, wm, wn, lane, acc, next, nxt < nsteps, pp);
     }
     slot = slot + 1 == NSX ? 0 : slot + 1;
   }
