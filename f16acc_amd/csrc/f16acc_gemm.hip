@@ -256,19 +256,16 @@ __device__ __forceinline__ i32x4 make_srd(const void* base) {
 // ds_reads; the loop waits for it explicitly (wait_vm0 + barrier) before the
 // stage it fills is read.  M0 carries the LDS address; one wait state is
 // required between writing M0 and the DMA that reads it.  The resource is
-// wave-uniform by construction; PIN (a K-contiguous b, whose stage copies go
-// out with no branch around them) pins it to scalar registers with
-// readfirstlane, where the compiler would otherwise keep a copy in vector
-// registers.  A row-major b's loop keeps the code it was measured with.
+// wave-uniform by construction; readfirstlane pins it to scalar registers,
+// where the compiler would otherwise keep copies in vector registers once a
+// stage's copies go out with no branch around them (and ran the row-major
+// loops 1.3-1.5 % slower without it).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved: the asm sets it itself
-template <bool PIN>
 __device__ __forceinline__ void lds_dma16(const i32x4& rsrc, int lds, int voff) {
-  i32x4 srd = rsrc;
-  if constexpr (PIN) {
+  i32x4 srd;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) srd[k] = __builtin_amdgcn_readfirstlane(rsrc[k]);
-  }
+  for (int k = 0; k < 4; ++k) srd[k] = __builtin_amdgcn_readfirstlane(rsrc[k]);
   asm volatile(
       "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
@@ -356,18 +353,16 @@ struct FastLoader {
     int wave;
     const FastLoader* ld;
     __device__ __forceinline__ void unit(int j) const {
-      constexpr bool kPin = C::BL == kKC;
       if (j < C::LA)
-        lds_dma16<kPin>(srd_at(ra, j * ld->a_step), lds + j * C::TG * 16, va);
+        lds_dma16(srd_at(ra, j * ld->a_step), lds + j * C::TG * 16, va);
       else if (j < C::LA + C::LBF || wave < C::LB_WAVES)  // wave-uniform
-        lds_dma16<kPin>(srd_at(rb, (j - C::LA) * ld->b_step), lds + C::A_STAGE + (j - C::LA) * C::TG * 16, vb);
+        lds_dma16(srd_at(rb, (j - C::LA) * ld->b_step), lds + C::A_STAGE + (j - C::LA) * C::TG * 16, vb);
     }
     __device__ __forceinline__ void all() const {
 #pragma unroll
       for (int j = 0; j < C::LA + C::LB; ++j) {
         unit(j);
-        // K-contiguous b: each unit's resource computed next to its copy
-        if constexpr (C::BL == kKC) __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_sched_barrier(0);  // each unit's resource computed next to its copy
       }
     }
   };
@@ -534,14 +529,13 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
   const char LDS_AS* bs = stage + C::A_STAGE;
   const int r16 = lane & 15, g = lane >> 4;
   // In the direct-to-LDS loop (DMA), the next stage's copies go out without
-  // a test of has_next where b is K-contiguous (except in a late K group):
-  // past the K range every unit reads zeros (offset kOob) into the slot the
-  // next stage would fill, which no wave reads again, and the stage stays
-  // one basic block (same bits; measured 1-2 % faster on 256x256 and
-  // 256x288, 6 % on 64x64, 0.2-1 % on the K-group tiles' early groups; none
-  // with a row-major b, and slower in the late groups).  The K loop waits
-  // for these copies before it hands the LDS on.
-  const bool copy_next = has_next || (DMA && C::BL == kKC);
+  // a test of has_next (except in a late K group): past the K range every
+  // unit reads zeros (offset kOob) into the slot the next stage would fill,
+  // which no wave reads again, and the stage stays one basic block (same
+  // bits; measured 1.3-2 % faster on 256x256 and 256x288, 6 % on 64x64,
+  // 0.2-1 % on the K-group tiles' early groups; slower in the late groups).
+  // The K loop waits for these copies before it hands the LDS on.
+  const bool copy_next = has_next || DMA;
   f16x8 af[C::FM][2];
   if (!CHUNKED) {
     // B one column ahead of its MFMAs; on 8-wave tiles the next stage's
