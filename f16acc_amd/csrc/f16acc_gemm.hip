@@ -761,11 +761,114 @@ __device__ __forceinline__ void group_reduce(char LDS_AS* smem, int g, int ltid,
 
 // The fast path's K loop over [kbeg, kend) for this thread's K group, then
 // the group reduction: group 0 ends with the tile's sum.
+
+// Chunked K loop of the 64x128-per-wave tiles (256x256, 256x288), with the
+// stage barrier moved from a stage's start to before its last column: a
+// two-stage ring, where a wave that reaches the barrier has read every
+// fragment of stage s (its last b column is in registers) and has its own
+// copies of stage s + 1 landed, so after the barrier it multiplies stage
+// s's last column while it reads stage s + 1's b(0) and, block by block
+// behind that column's MFMAs, stage s + 1's A fragments.  A stage then
+// starts with its fragments in registers instead of waiting on the LDS
+// behind every wave's first reads.  The copies of stage s + 2 go out one a
+// step from the start of stage s + 1 into the slot stage s used, so that
+// they land before that stage's barrier, three quarters of a stage later
+// (spread over its first half, as k_loop_fast does, they left too little
+// time where the operands come from HBM: the lm_head shape ran 3 % slower).
+// Same operations in the same order as k_loop_fast (same bits); measured
+// 0.9-1.4 % faster on 4096^3, 8192^3 and Qwen gate/up, level on the lm_head
+// shape.  (FP32 accumulation keeps k_loop_fast: there this form ran 2-6 %
+// slower.)
+template <class C>
+__device__ __forceinline__ void step_cross(int t, const f16x8 (&af)[C::FM][2], const f16x8 (&bc)[2], const f16x8& sel,
+                                           f32x4 (&acc)[C::FM][C::FN], Pipe<C>& pp) {
+  const int i = t % C::FM;
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  __builtin_amdgcn_sched_barrier(0);
+  pp.p0[t % 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bc[0], af[i][0], zero, 0, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  pipe_round<C>(pp, t - 2, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  pp.p1[t % 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bc[1], af[i][1], zero, 0, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  pipe_round<C>(pp, t - 2, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  pipe_sum<C>(pp, sel, t - 3, acc);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <class C>
+__device__ __forceinline__ void k_loop_cross(const Params& p, int64_t m0, int64_t n0, int64_t kbeg, int64_t kend,
+                                             char LDS_AS* smem, FastLoader<C>& ld, int wave, int wm, int wn, int lane,
+                                             f32x4 (&acc)[C::FM][C::FN]) {
+  constexpr int T = C::FM * C::FN, kUnits = C::LA + C::LB;
+  static_assert(kUnits <= T - C::FM, "copies must go out before the last column");
+  static_assert(C::NS == 2 && C::KG == 1 && C::FM > 1, "two-stage ring, one K group");
+  const int64_t nsteps = kend > kbeg ? (kend - kbeg + kStageK - 1) / kStageK : 0;
+  if (nsteps <= 0) return;
+  const int r16 = lane & 15, g = lane >> 4;
+  ld.issue(p, m0, n0, kbeg, kend, smem, wave);
+  wait_vm0();
+  __syncthreads();
+  f16x8 af[C::FM][2], bc[2], bn[2];
+  bc[0] = read_b<C>(smem + C::A_STAGE, wn, 0, 0, lane);
+  bc[1] = read_b<C>(smem + C::A_STAGE, wn, 0, 1, lane);
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) af[i][c] = read_kc<C>(smem, wm * C::WTM + 16 * i + r16, 4 * c + g);
+  const f16x8 sel = chunk_pair_selector(lane);
+  Pipe<C> pp;
+  int slot = 0;
+  for (int64_t s = 0; s < nsteps; ++s) {
+    const char LDS_AS* bs = smem + slot * C::STAGE + C::A_STAGE;
+    char LDS_AS* nslot = smem + (slot ^ 1) * C::STAGE;
+    // the copies of stage s + 1 (past the K range they read zeros, offset
+    // kOob, into a slot no wave reads again: no branch in the stage)
+    const typename FastLoader<C>::Stage next = ld.stage(p, m0, n0, kbeg + (s + 1) * kStageK, kend, nslot, wave);
+#pragma unroll
+    for (int t = 0; t < T - C::FM; ++t) {
+      const int i = t % C::FM, j = t / C::FM;
+      if (t < kUnits) next.unit(t);  // one copy a step, from the stage's start
+      if (i == 1) {  // b(j + 1) behind the first row's A reads in the LDS queue
+        bn[0] = read_b<C>(bs, wn, j + 1, 0, lane);
+        bn[1] = read_b<C>(bs, wn, j + 1, 1, lane);
+      }
+      step_cross<C>(t, af, bc, sel, acc, pp);
+      if (i == C::FM - 1) {
+        bc[0] = bn[0];
+        bc[1] = bn[1];
+      }
+    }
+    wait_vm0();       // this wave's copies of stage s + 1
+    __syncthreads();  // everyone's, and every read of stage s's slot done
+    bn[0] = read_b<C>(nslot + C::A_STAGE, wn, 0, 0, lane);
+    bn[1] = read_b<C>(nslot + C::A_STAGE, wn, 0, 1, lane);
+#pragma unroll
+    for (int t = T - C::FM; t < T; ++t) {
+      const int i = t % C::FM;
+      step_cross<C>(t, af, bc, sel, acc, pp);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) af[i][c] = read_kc<C>(nslot, wm * C::WTM + 16 * i + r16, 4 * c + g);
+    }
+    bc[0] = bn[0];
+    bc[1] = bn[1];
+    slot ^= 1;
+  }
+  pipe_drain<C>(pp, lane, acc);
+  wait_vm0();       // the last stage's copies past the K range
+  __syncthreads();  // LDS free for the store's staging
+}
+
 template <class C, bool CHUNKED>
 __device__ __forceinline__ void k_groups_fast(const Params& p, int64_t m0, int64_t n0, int64_t kbeg, int64_t kend,
                                               char LDS_AS* smem, FastLoader<C>& ld, int g, int ltid, int lw, int wm,
                                               int wn, int lane, f32x4 (&acc)[C::FM][C::FN],
                                               int LDS_AS* flag = nullptr) {
+  if constexpr (CHUNKED && C::KG == 1 && C::FM * C::FN >= 32) {
+    k_loop_cross<C>(p, m0, n0, kbeg, kend, smem, ld, lw, wm, wn, lane, acc);
+    return;
+  }
   int64_t gbeg = kbeg, gend = kend, iters = 0;
   if (C::KG > 1) iters = group_range<C>(kbeg, kend, g, &gbeg, &gend);
   if (C::SPLIT && g >= C::KG / 2)  // wave-uniform
