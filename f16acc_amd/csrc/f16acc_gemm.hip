@@ -515,6 +515,30 @@ __device__ __forceinline__ void pipe_drain(Pipe<C>& pp, int lane, f32x4 (&acc)[C
   }
 }
 
+// Step t of a stage's chunk pipeline (block (i, j) = (t % FM, t / FM)): the
+// block's two chunk MFMAs with the rounding of block t-2 between them (half
+// after each), then the selector MFMA of block t-3, so that no instruction
+// reads an MFMA result fewer than three MFMAs old; sched_barrier fences hold
+// that order (left to itself the scheduler puts each conversion right behind
+// the MFMA that produces its input and pads with s_nop).
+template <class C>
+__device__ __forceinline__ void chunk_step(int t, const f16x8 (&af)[C::FM][2], const f16x8 (&bc)[2], const f16x8& sel,
+                                           f32x4 (&acc)[C::FM][C::FN], Pipe<C>& pp) {
+  const int i = t % C::FM;
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  __builtin_amdgcn_sched_barrier(0);
+  pp.p0[t % 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bc[0], af[i][0], zero, 0, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  pipe_round<C>(pp, t - 2, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  pp.p1[t % 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bc[1], af[i][1], zero, 0, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  pipe_round<C>(pp, t - 2, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  pipe_sum<C>(pp, sel, t - 3, acc);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // LATE: a late K group of a split-phase tile (Cfg::SPLIT) issues the copies
 // `next` after the stage's MFMAs instead of before them.  DMA: `next` is a
 // real stage of the direct-to-LDS loader (k_loop_fast); the register-staged
@@ -575,17 +599,11 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
     return;
   }
   // Chunked: blocks t = 0 .. FM*FN-1 (i = t % FM fastest), software
-  // pipelined four deep.  Step t issues block t's two chunk MFMAs with the
-  // rounding of block t-2 between them (half after each), then the selector
-  // MFMA of block t-3: every instruction reads an MFMA result at least three
-  // MFMAs old, so nothing waits on the matrix pipe.  The first steps of a
-  // stage finish the previous stage's last blocks (carry), so the pipeline
-  // only drains once, after the K loop.  sched_barrier fences keep that
-  // order (left to itself the scheduler puts each conversion right behind
-  // the MFMA that produces its input and pads with s_nop).
+  // pipelined four deep (chunk_step).  The first steps of a stage finish the
+  // previous stage's last blocks (carry), so the pipeline only drains once,
+  // after the K loop.
   static_assert(C::FM * C::FN % 4 == 0, "block count must be a multiple of the partials ring");
   constexpr int T = C::FM * C::FN;
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   const f16x8 sel = chunk_pair_selector(lane);  // loop invariant: hoisted out of the K loop
   // LDS reads are spread over the stage instead of issued in one burst at
   // its start (all waves of the workgroup start a stage together after the
@@ -626,17 +644,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
       bnext[0] = read_b<C>(bs, wn, j + 1, 0, lane);
       bnext[1] = read_b<C>(bs, wn, j + 1, 1, lane);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    pp.p0[t % 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bcur[0], af[i][0], zero, 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    pipe_round<C>(pp, t - 2, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    pp.p1[t % 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bcur[1], af[i][1], zero, 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    pipe_round<C>(pp, t - 2, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    pipe_sum<C>(pp, sel, t - 3, acc);
-    __builtin_amdgcn_sched_barrier(0);
+    chunk_step<C>(t, af, bcur, sel, acc, pp);
     if (i == C::FM - 1 && j + 1 < C::FN) {
       bcur[0] = bnext[0];
       bcur[1] = bnext[1];
@@ -779,23 +787,6 @@ __device__ __forceinline__ void group_reduce(char LDS_AS* smem, int g, int ltid,
 // 0.9-1.4 % faster on 4096^3, 8192^3 and Qwen gate/up, level on the lm_head
 // shape.  (FP32 accumulation keeps k_loop_fast: there this form ran 2-6 %
 // slower.)
-template <class C>
-__device__ __forceinline__ void step_cross(int t, const f16x8 (&af)[C::FM][2], const f16x8 (&bc)[2], const f16x8& sel,
-                                           f32x4 (&acc)[C::FM][C::FN], Pipe<C>& pp) {
-  const int i = t % C::FM;
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  __builtin_amdgcn_sched_barrier(0);
-  pp.p0[t % 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bc[0], af[i][0], zero, 0, 0, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  pipe_round<C>(pp, t - 2, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  pp.p1[t % 4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bc[1], af[i][1], zero, 0, 0, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  pipe_round<C>(pp, t - 2, 1);
-  __builtin_amdgcn_sched_barrier(0);
-  pipe_sum<C>(pp, sel, t - 3, acc);
-  __builtin_amdgcn_sched_barrier(0);
-}
 
 template <class C>
 __device__ __forceinline__ void k_loop_cross(const Params& p, int64_t m0, int64_t n0, int64_t kbeg, int64_t kend,
@@ -834,7 +825,7 @@ __device__ __forceinline__ void k_loop_cross(const Params& p, int64_t m0, int64_
         bn[0] = read_b<C>(bs, wn, j + 1, 0, lane);
         bn[1] = read_b<C>(bs, wn, j + 1, 1, lane);
       }
-      step_cross<C>(t, af, bc, sel, acc, pp);
+      chunk_step<C>(t, af, bc, sel, acc, pp);
       if (i == C::FM - 1) {
         bc[0] = bn[0];
         bc[1] = bn[1];
@@ -847,7 +838,7 @@ __device__ __forceinline__ void k_loop_cross(const Params& p, int64_t m0, int64_
 #pragma unroll
     for (int t = T - C::FM; t < T; ++t) {
       const int i = t % C::FM;
-      step_cross<C>(t, af, bc, sel, acc, pp);
+      chunk_step<C>(t, af, bc, sel, acc, pp);
 #pragma unroll
       for (int c = 0; c < 2; ++c) af[i][c] = read_kc<C>(nslot, wm * C::WTM + 16 * i + r16, 4 * c + g);
     }
