@@ -357,6 +357,40 @@ def test_every_tile_redoes_overflow_in_every_wave(tile, wm, wn):
     assert rel(c.cpu(), ref) < TOL
 
 
+@pytest.mark.parametrize("tile, wm, wn", _wave_cases(["256x256", "256x288"]))
+def test_overflow_in_the_last_column_of_the_last_stage(tile, wm, wn):
+    """The chunked 256x256 and 256x288 loops multiply a stage's last column
+    after the stage barrier, while they read the next stage's fragments (past
+    the last stage: a slot of zeros).  The overflow closed form (reference
+    tests/test_f16acc.py:91-101) lies in the last stage only (K = 320: chunks
+    8 and 9, the earlier chunks of those rows are zeros), in the last row block
+    and the last column of one wave's sub-tile of tile (1, 1): exactly that
+    tile is flagged and its redone block is exact; both b layouts for 256x256."""
+    bm, bn = tile_dims(tile)
+    wmc, wnc = WAVES[tile]
+    M, N, K = 2 * bm, 2 * bn, 320
+    a = rnd((M, K), 44, 0.5)
+    b = rnd((K, N), 45, 0.5)
+    r0 = bm + wm * (bm // wmc) + bm // wmc - 14  # rows 50-59 of the wave's 64: its last row block
+    c0 = bn + wn * (bn // wnc) + bn // wnc - 12  # columns in the wave's last 16-column block
+    a[r0:r0 + 10, :] = 0.0
+    a[r0:r0 + 10, 256:] = 100.0
+    b[:, c0:c0 + 10] = 0.0
+    b[256:288, c0:c0 + 10], b[288:320, c0:c0 + 10] = 30.0, -30.0
+    b[319, c0:c0 + 10] = -29.0
+    ga = a.cuda()
+    for b_row_major in ((False, True) if tile == "256x256" else (False,)):
+        gb = b.cuda() if b_row_major else b.t().contiguous().cuda().t()
+        cfg = tile_config(ga, gb, tile)
+        assert cfg["tile"] == tile
+        c, flags = mm_flags(ga, gb, torch.float32, tile=tile)
+        ref, rflags = oracle(a, b, torch.float32, cfg)
+        assert int(rflags.sum()) == 1 and rflags[1, 1] == 1
+        assert torch.equal(flags.cpu(), rflags), (tile, wm, wn, b_row_major)
+        assert torch.all(c[r0:r0 + 10, c0:c0 + 10].cpu() == 100.0)
+        assert rel(c.cpu(), ref) < TOL
+
+
 K_GROUPS = {"128x96k2": 2, "64x32k4": 4}
 
 
