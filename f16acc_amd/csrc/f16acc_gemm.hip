@@ -48,6 +48,7 @@
 #include <stdint.h>
 
 #include <atomic>
+#include <type_traits>
 
 #include "f16acc.h"
 
@@ -539,16 +540,24 @@ __device__ __forceinline__ void chunk_step(int t, const f16x8 (&af)[C::FM][2], c
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// The `next` stage of the loops that fill the LDS through registers
+// (k_loop_reg, k_loop_generic): they issue no global -> LDS copy, and this
+// type has no copy to issue.
+struct NoCopies {
+  __device__ __forceinline__ void unit(int) const {}
+  __device__ __forceinline__ void all() const {}
+};
+
 // LATE: a late K group of a split-phase tile (Cfg::SPLIT) issues the copies
-// `next` after the stage's MFMAs instead of before them.  DMA: `next` is a
-// real stage of the direct-to-LDS loader (k_loop_fast); the register-staged
-// and gather loops pass an empty one with has_next false, and no copy may
-// go out.
-template <class C, bool CHUNKED, bool LATE = false, bool DMA = false>
+// `next` after the stage's MFMAs instead of before them.  Next is
+// FastLoader<C>::Stage in the direct-to-LDS loop (k_loop_fast), NoCopies in
+// the others.
+template <class C, bool CHUNKED, bool LATE = false, class Next = NoCopies>
 __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, int wn, int lane,
-                                              f32x4 (&acc)[C::FM][C::FN],
-                                              const typename FastLoader<C>::Stage& next, bool has_next,
+                                              f32x4 (&acc)[C::FM][C::FN], const Next& next, bool has_next,
                                               Pipe<C>& pp) {
+  constexpr bool DMA = !std::is_same<Next, NoCopies>::value;
+  static_assert(!DMA || std::is_same<Next, typename FastLoader<C>::Stage>::value, "copies come from FastLoader");
   const char LDS_AS* as = stage;
   const char LDS_AS* bs = stage + C::A_STAGE;
   const int r16 = lane & 15, g = lane >> 4;
@@ -558,7 +567,9 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
   // which no wave reads again, and the stage stays one basic block (same
   // bits; measured 1.3-2 % faster on 256x256 and 256x288, 6 % on 64x64,
   // 0.2-1 % on the K-group tiles' early groups; slower in the late groups).
-  // The K loop waits for these copies before it hands the LDS on.
+  // The K loop waits for these copies before it hands the LDS on.  (A late
+  // group copies after the stage, behind a test of has_next, and never
+  // spreads its copies over the stage.)
   const bool copy_next = has_next || DMA;
   f16x8 af[C::FM][2];
   if (!CHUNKED) {
@@ -583,7 +594,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
         bn0 = read_b<C>(bs, wn, j + 1, 0, lane);
         bn1 = read_b<C>(bs, wn, j + 1, 1, lane);
       }
-      if (kSpread && copy_next && j < kDmaCols) {
+      if (kSpread && !LATE && copy_next && j < kDmaCols) {
 #pragma unroll
         for (int u = 0; u < kPerCol; ++u)
           if (j * kPerCol + u < kUnits) next.unit(j * kPerCol + u);
@@ -635,7 +646,7 @@ __device__ __forceinline__ void compute_stage(const char LDS_AS* stage, int wm, 
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const int i = t % C::FM, j = t / C::FM;
-    if (kSpread && copy_next && t % kDmaEvery == 0 && t / kDmaEvery < kUnits) next.unit(t / kDmaEvery);
+    if (kSpread && !LATE && copy_next && t % kDmaEvery == 0 && t / kDmaEvery < kUnits) next.unit(t / kDmaEvery);
     if (j == 0 && i + 1 < C::FM) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) af[i + 1][c] = read_kc<C>(as, wm * C::WTM + 16 * (i + 1) + r16, 4 * c + g);
@@ -696,7 +707,7 @@ __device__ __forceinline__ void k_loop_fast(const Params& p, int64_t m0, int64_t
       const int nslot = slot == 0 ? NSX - 1 : slot - 1;  // (s + NSX - 1) % NSX
       const typename FastLoader<C>::Stage next =
           ld.stage(p, m0, n0, kbeg + nxt * kStageK, kend, smem + nslot * C::STAGE, wave);
-      compute_stage<C, CHUNKED, LATE, true>(smem + slot * C::STAGE, wm, wn, lane, acc, next, nxt < nsteps, pp);
+      compute_stage<C, CHUNKED, LATE>(smem + slot * C::STAGE, wm, wn, lane, acc, next, nxt < nsteps, pp);
     }
     slot = slot + 1 == NSX ? 0 : slot + 1;
   }
@@ -1009,10 +1020,9 @@ __device__ __forceinline__ void k_loop_reg(const Params& p, int64_t m0, int64_t 
   if (nsteps > 1) load(kbeg + kStageK);
   __syncthreads();
   Pipe<C> pp;
-  const typename FastLoader<C>::Stage none{};
   for (int64_t s = 0; s < nsteps; ++s) {
     char LDS_AS* cur = smem + (s & 1) * C::STAGE;
-    compute_stage<C, CHUNKED>(cur, wm, wn, lane, acc, none, false, pp);
+    compute_stage<C, CHUNKED>(cur, wm, wn, lane, acc, NoCopies{}, false, pp);
     if (s + 1 < nsteps) {
       rl.store(p, m0, n0, buf, smem + ((s + 1) & 1) * C::STAGE, tid);
       if (s + 2 < nsteps) load(kbeg + (s + 2) * kStageK);
@@ -1061,8 +1071,7 @@ __device__ __forceinline__ void k_loop_generic(const Params& p, int64_t m0, int6
   for (int64_t s = 0; s < nsteps; ++s) {
     stage_generic<C>(p, m0, n0, s * kStageK, smem, tid);
     __syncthreads();
-    const typename FastLoader<C>::Stage none{};
-    compute_stage<C, CHUNKED>(smem, wm, wn, lane, acc, none, false, pp);
+    compute_stage<C, CHUNKED>(smem, wm, wn, lane, acc, NoCopies{}, false, pp);
     __syncthreads();
   }
   if (CHUNKED && nsteps > 0) pipe_drain<C>(pp, lane, acc);
@@ -1602,18 +1611,39 @@ inline int reg_layout(int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sb
   return -1;
 }
 
-inline int fast_layout(int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn, const void* a,
-                       const void* b, int bm, int bn) {
-  const bool a_ok = (sak == 1 || K <= 1) && sam % 8 == 0 && ((uintptr_t)a % 16) == 0 && K % 8 == 0 &&
-                    (int64_t)bm * sam * 2 + 4 * kStageK < kOob;
+// The direct-to-LDS copies clip each operand by one buffer record count per
+// tile and stage (FastLoader): the bytes from the tile's first row to the end
+// of its last row inside M (N for a K-contiguous b; for a row-major b, k-rows
+// inside the stage's K range).  That clip is exact only when rows do not
+// overlap: a row stride of at least a row (sam >= K for a, sbn >= K for a
+// K-contiguous b, sbk >= N for a row-major b).  Broadcast views (stride 0,
+// x.expand(M, K)) and sliding windows (stride < row) go to the register-staged
+// loader, a packed copy or the gather kernel, which read every row by its own
+// address, as the reference's pointer arithmetic does (kernel.py:41-47).
+inline int fast_layout(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
+                       const void* a, const void* b, int bm, int bn) {
+  const bool a_ok = (sak == 1 || K <= 1) && sam % 8 == 0 && (M <= 1 || sam >= K) && ((uintptr_t)a % 16) == 0 &&
+                    K % 8 == 0 && (int64_t)bm * sam * 2 + 4 * kStageK < kOob;
   if (!a_ok) return -1;
-  const bool b_kc = (sbk == 1 || K <= 1) && sbn % 8 == 0 && ((uintptr_t)b % 16) == 0 && K % 8 == 0 &&
-                    (int64_t)bn * sbn * 2 + 4 * kStageK < kOob;
+  const bool b_kc = (sbk == 1 || K <= 1) && sbn % 8 == 0 && (N <= 1 || sbn >= K) && ((uintptr_t)b % 16) == 0 &&
+                    K % 8 == 0 && (int64_t)bn * sbn * 2 + 4 * kStageK < kOob;
   if (b_kc) return kKC;
-  const bool b_nc = (sbn == 1 || N <= 1) && sbk % 8 == 0 && ((uintptr_t)b % 16) == 0 && N % 8 == 0 &&
-                    (int64_t)kStageK * sbk * 2 + 2 * bn < kOob;
+  const bool b_nc = (sbn == 1 || N <= 1) && sbk % 8 == 0 && (K <= 1 || sbk >= N) && ((uintptr_t)b % 16) == 0 &&
+                    N % 8 == 0 && (int64_t)kStageK * sbk * 2 + 2 * bn < kOob;
   if (b_nc) return kNC;
   return -1;
+}
+
+// The stride of an extent-1 dimension addresses nothing, and torch reports
+// any value for it (x[:1] keeps the parent's row stride, v.expand(1, K) has
+// 0).  Every planner and kernel sees it replaced by a plain row length, so
+// a single row takes the same path as a contiguous one (its record count is
+// then the row itself).
+inline void canon_strides(int64_t M, int64_t N, int64_t K, int64_t* sam, int64_t* sbk, int64_t* sbn) {
+  const int64_t row = (K + 7) / 8 * 8;
+  if (M <= 1) *sam = row;
+  if (N <= 1) *sbn = row;
+  if (K <= 1) *sbk = (N + 7) / 8 * 8;
 }
 
 // Relative throughput of one CU on each fast tile: its chunked MFMA work rate
@@ -1799,12 +1829,12 @@ struct TailPlan {
 inline bool plan_tail(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
                       const void* a, const void* b, int cus, TailPlan* plan) {
   const TileInfo& t = kTiles[F16ACC_TILE_256x256];
-  if (fast_layout(N, K, sam, sak, sbk, sbn, a, b, t.bm, t.bn) < 0) return false;
+  if (fast_layout(M, N, K, sam, sak, sbk, sbn, a, b, t.bm, t.bn) < 0) return false;
   const int64_t tm = cdiv(M, t.bm), tn = cdiv(N, t.bn), tiles = tm * tn;
   const int64_t rounds = tiles / cus;
   if (rounds < 1 || tiles % cus == 0) return false;
   // no cut where the table takes 256x288 for the whole problem
-  if (fast_layout(N, K, sam, sak, sbk, sbn, a, b, 256, 288) == kKC &&
+  if (fast_layout(M, N, K, sam, sak, sbk, sbn, a, b, 256, 288) == kKC &&
       choose_tile(M, N, K, cus, nullptr, true) == F16ACC_TILE_256x288)
     return false;
   double whole = 0;
@@ -1845,9 +1875,9 @@ inline Choice choose(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak, 
                      const void* a, const void* b, int forced_tile, bool kgroups = true) {
   int id = forced_tile >= 0 ? forced_tile
                             : choose_tile(M, N, K, cu_count(), nullptr,
-                                          kgroups && fast_layout(N, K, sam, sak, sbk, sbn, a, b, 128, 128) == kKC);
+                                          kgroups && fast_layout(M, N, K, sam, sak, sbk, sbn, a, b, 128, 128) == kKC);
   if (id == F16ACC_TILE_GENERIC) return Choice{id, F16ACC_FAMILY_GENERIC, kKC};
-  const int bl = fast_layout(N, K, sam, sak, sbk, sbn, a, b, kTiles[id].bm, kTiles[id].bn);
+  const int bl = fast_layout(M, N, K, sam, sak, sbk, sbn, a, b, kTiles[id].bm, kTiles[id].bn);
   // The K-group tiles run on the direct-to-LDS copies with a K-contiguous b
   // only: other operands take the nearest tile without K groups (128x128,
   // 64x64).
@@ -2004,12 +2034,21 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
   if (forced_tile < -1 || forced_tile >= F16ACC_NUM_TILES) return F16ACC_E_ARG;
   if (M == 0 || N == 0) return 0;  // nothing to write (Triton skips an empty grid too)
   if (!c || (K > 0 && (!a || !b))) return F16ACC_E_ARG;
+  canon_strides(M, N, K, &sam, &sbk, &sbn);
   // A caller asking for tile flags gets one grid, the one f16acc_tile_config
   // describes; otherwise a ragged last 256x256 round may become a second launch.
   TailPlan tp;
   if (forced_tile < 0 && !tile_flags && K > 0 && plan_tail(M, N, K, sam, sak, sbk, sbn, a, b, cu_count(), &tp)) {
     const int esize = out_dtype == F16ACC_OUT_F32 ? 4 : 2;
     const int64_t at = tp.at;
+    // A fixed workspace must hold the second launch's split plan (the first,
+    // on 256x256, never splits): checked before anything is launched.
+    if (strict_ws) {
+      const Choice tc = tp.rows ? choose(M - at, N, K, sam, sak, sbk, sbn, (const f16*)a + at * sam, b, -1, false)
+                                : choose(M, N - at, K, sam, sak, sbk, sbn, a, (const f16*)b + at * sbn, -1, false);
+      const SplitPlan ts = tp.rows ? plan_split(tc, M - at, N, K, cu_count()) : plan_split(tc, M, N - at, K, cu_count());
+      if (ts.bytes > ws_bytes) return F16ACC_E_SCRATCH;
+    }
     if (tp.rows) {
       const int rc = gemm_impl(a, b, bias, c, nullptr, at, N, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked,
                                stream, F16ACC_TILE_256x256);
@@ -2162,6 +2201,7 @@ int f16acc_tail_split(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak,
                       const void* a, const void* b, int64_t* nsplit) {
   if (M < 0 || N < 0 || K < 0 || !nsplit) return F16ACC_E_ARG;
   *nsplit = 0;
+  canon_strides(M, N, K, &sam, &sbk, &sbn);
   if (M > 0 && N > 0 && K > 0) {
     TailPlan tp;
     if (plan_tail(M, N, K, sam, sak, sbk, sbn, a, b, cu_count(), &tp)) *nsplit = tp.rows ? -tp.at : tp.at;
@@ -2173,6 +2213,7 @@ int f16acc_tile_config(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t sak
                        const void* a, const void* b, int forced_tile, int* tile, int* bm, int* bn,
                        int64_t* tiles_m, int64_t* tiles_n, int* family, int* threads) {
   if (M < 0 || N < 0 || K < 0 || forced_tile < -1 || forced_tile >= F16ACC_NUM_TILES) return F16ACC_E_ARG;
+  canon_strides(M, N, K, &sam, &sbk, &sbn);
   const Choice ch = choose(M, N, K, sam, sak, sbk, sbn, a, b, forced_tile);
   const TileInfo& t = kTiles[ch.tile];
   if (tile) *tile = ch.tile;
@@ -2223,6 +2264,7 @@ int f16acc_workspace_size(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t 
   if (M < 0 || N < 0 || K < 0 || !bytes) return F16ACC_E_ARG;
   *bytes = 0;
   if (M == 0 || N == 0) return 0;
+  canon_strides(M, N, K, &sam, &sbk, &sbn);
   const Choice ch = choose(M, N, K, sam, sak, sbk, sbn, a, b, -1);
   *bytes = plan_split(ch, M, N, K, cu_count()).bytes;
   return 0;

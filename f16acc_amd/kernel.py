@@ -103,8 +103,9 @@ def _workspace(a, b, M, N, K):
 
 def _capture_id(stream):
     """Sequence id of the HIP graph capture running on `stream`
-    (hipStreamGetCaptureInfo); a fresh key where the runtime will not say, so
-    that such a call gets a workspace of its own."""
+    (hipStreamGetCaptureInfo).  Called only while torch reports a capture on
+    that stream; a runtime that then names no active capture is an error
+    (a fresh key per call would leave one workspace per call behind)."""
     global _hip
     if _hip is None:
         _hip = ctypes.CDLL("libamdhip64.so")
@@ -112,8 +113,10 @@ def _capture_id(stream):
                                                  ctypes.POINTER(ctypes.c_ulonglong)]
         _hip.hipStreamGetCaptureInfo.restype = ctypes.c_int
     status, cid = ctypes.c_int(), ctypes.c_ulonglong()
-    if _hip.hipStreamGetCaptureInfo(stream, ctypes.byref(status), ctypes.byref(cid)) != 0 or status.value != 1:
-        return object()  # hipStreamCaptureStatusActive is 1
+    rc = _hip.hipStreamGetCaptureInfo(stream, ctypes.byref(status), ctypes.byref(cid))
+    if rc != 0 or status.value != 1:  # hipStreamCaptureStatusActive is 1
+        raise RuntimeError(f"f16acc: no HIP graph capture id for the capturing stream (hipError {rc}, "
+                           f"status {status.value})")
     return cid.value
 
 
@@ -138,17 +141,30 @@ def mm_bias(a, b, bias, out_dtype=torch.float16, chunked=True):
     return c
 
 
+def _canon(stride, extent, row):
+    """The stride the library plans with: an extent-1 dimension's stride
+    addresses nothing, so it counts as a plain row length `row`."""
+    return stride if extent > 1 else row
+
+
 def _fast_a(a, K):
-    """a [M, K] as the fast kernels read it: K-contiguous 16-byte aligned rows."""
-    return K % 8 == 0 and (a.stride(1) == 1 or K <= 1) and a.stride(0) % 8 == 0 and a.data_ptr() % 16 == 0
+    """a [M, K] as the fast kernels read it: K-contiguous 16-byte aligned rows
+    that do not overlap (row stride >= K; a broadcast row, stride 0, or a
+    sliding window does not qualify: the copies clip a tile by one record
+    count, which needs disjoint rows)."""
+    sam = _canon(a.stride(0), a.shape[0], -(-K // 8) * 8)
+    return K % 8 == 0 and (a.stride(1) == 1 or K <= 1) and sam % 8 == 0 and sam >= K and a.data_ptr() % 16 == 0
 
 
 def _fast_b(b, K, N):
-    """b [K, N]: K-contiguous columns (w.t()) or N-contiguous rows, 16-byte aligned."""
+    """b [K, N]: K-contiguous columns (w.t()) or N-contiguous rows, 16-byte
+    aligned, with disjoint rows (sbn >= K, or sbk >= N for a row-major b)."""
     if b.data_ptr() % 16:
         return False
-    kc = K % 8 == 0 and (b.stride(0) == 1 or K <= 1) and b.stride(1) % 8 == 0
-    nc = N % 8 == 0 and (b.stride(1) == 1 or N <= 1) and b.stride(0) % 8 == 0
+    sbk = _canon(b.stride(0), K, -(-N // 8) * 8)
+    sbn = _canon(b.stride(1), N, -(-K // 8) * 8)
+    kc = K % 8 == 0 and (sbk == 1 or K <= 1) and sbn % 8 == 0 and sbn >= K
+    nc = N % 8 == 0 and (sbn == 1 or N <= 1) and sbk % 8 == 0 and sbk >= N
     return kc or nc
 
 

@@ -66,6 +66,43 @@ def chunked_sum(a16, b16, chunk=CHUNK, mode="round_once", group=8):
     return s
 
 
+def paired_sum(a16, b16, kgroups=1, exact_partials=False):
+    """The same FP16-rounded chunk partials as chunked_sum (round_once), summed
+    in the order of a kernel that adds chunk pairs: for each 64-long K stage,
+    s = fp32(s + H_2p + H_2p+1) with one rounding, stages in K order.  With
+    kgroups > 1 the stages are dealt to kgroups consecutive ranges of
+    ceil(stages / kgroups) each, every range summed this way from zero, and
+    the range sums added in range order in FP32.  exact_partials: each chunk's
+    FP32 partial is the exactly summed dot product rounded once to FP32
+    (instead of torch's FP32 matmul).
+
+    This is not the reference's order (that is chunked_sum: one chunk at a
+    time, kernel.py:49); it differs from it by FP32 reassociation only, and is
+    equal to it wherever every sum is exact.  Tests use it to compare the
+    kernel's bits, where the reference's order only bounds them."""
+    M, K = a16.shape
+    N = b16.shape[1]
+    nst = (K + 2 * CHUNK - 1) // (2 * CHUNK)
+    per = -(-nst // kgroups) if nst else 0
+    total = torch.zeros(M, N, dtype=torch.float32)
+    for g in range(kgroups):
+        s = torch.zeros(M, N, dtype=torch.float64)  # FP32 values, added exactly in FP64
+        for st in range(g * per, min(nst, (g + 1) * per)):
+            acc = s.clone()
+            for k0 in (2 * st * CHUNK, (2 * st + 1) * CHUNK):
+                if k0 >= K:
+                    continue
+                k1 = min(K, k0 + CHUNK)
+                if exact_partials:
+                    p = (a16[:, k0:k1].double() @ b16[k0:k1, :].double()).float()
+                else:
+                    p = a16[:, k0:k1].float() @ b16[k0:k1, :].float()
+                acc += _f16(p).double()
+            s = acc.float().double()  # one rounding per stage
+        total = total + s.float() if g else s.float()
+    return total
+
+
 def tile_flags(s, bm, bn):
     """One flag per (bm x bn) tile, row-major tile order: any element not
     finite (kernel.py:70-71)."""

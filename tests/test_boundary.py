@@ -202,6 +202,54 @@ def test_misaligned_pointer_is_packed_read_in_place_or_gathered():
         assert tile_config(_Fake((64, 64), (64, 1), ptr=4098), _Fake((64, 64), b_strides), tile)["family"] == "fast"
 
 
+_OVERLAP = {  # (a strides, b strides) of [512, 320] @ [320, 576] views whose rows overlap
+    "a_broadcast": ((0, 1), (576, 1)),          # x.expand(M, K)
+    "a_window": ((8, 1), (1, 320)),             # rows 8 apart (unfold)
+    "b_broadcast_rowmajor": ((320, 1), (0, 1)),  # v.expand(K, N)
+    "b_broadcast_wt": ((320, 1), (1, 0)),        # v.expand(N, K).t()
+    "b_window_wt": ((320, 1), (1, 8)),           # weight rows 8 apart, as w.t()
+    "b_window_rowmajor": ((320, 1), (8, 1)),     # k-rows 8 apart
+}
+
+
+@pytest.mark.parametrize("case", list(_OVERLAP))
+def test_overlapping_rows_never_take_the_direct_copies(case):
+    """The copies clip a tile by one record count, exact only for disjoint
+    rows: with a row stride of 0 or under a row the library routes every
+    table pick and every forced tile elsewhere (register-staged, gather), and
+    mm's own test of the layouts agrees (it packs such operands or leaves
+    them to the library)."""
+    from f16acc_amd.kernel import _fast_a, _fast_b
+
+    sa, sb = _OVERLAP[case]
+    M, N, K = 512, 576, 320
+    fam = ctypes.c_int()
+    for tile in [-1] + [i for i, t in enumerate(_lib.TILES) if t != "generic"]:
+        _lib.check(_lib.tile_config(M, N, K, *sa, *sb, 4096, 8192, tile, None, None, None, None, None,
+                                    ctypes.byref(fam), None))
+        assert fam.value != 0, (case, tile)  # not F16ACC_FAMILY_FAST
+    assert not (_fast_a(_Fake((M, K), sa), K) and _fast_b(_Fake((K, N), sb), K, N))
+
+
+@pytest.mark.parametrize("M, N, K, sa, sb", [
+    (1, 1536, 1536, (0, 1), (1, 1536)),    # one row broadcast from a vector: stride 0 addresses nothing
+    (1, 1536, 1536, (4096, 1), (1, 1536)),  # x[:1] of a wider buffer
+    (512, 1, 1536, (1536, 1), (1, 1)),      # b a contiguous [K, 1] column
+    (512, 1, 1536, (1536, 1), (1, 0)),      # b = v.expand(1, K).t()
+])
+def test_single_rows_and_columns_take_the_direct_copies(M, N, K, sa, sb):
+    """The stride of an extent-1 dimension is replaced by a row length before
+    planning, so a single row or column keeps the fast path whatever stride
+    torch reports for it (and its record count covers the row)."""
+    from f16acc_amd.kernel import _fast_a, _fast_b
+
+    fam = ctypes.c_int()
+    _lib.check(_lib.tile_config(M, N, K, *sa, *sb, 4096, 8192, -1, None, None, None, None, None,
+                                ctypes.byref(fam), None))
+    assert fam.value == 0
+    assert _fast_a(_Fake((M, K), sa), K) and _fast_b(_Fake((K, N), sb), K, N)
+
+
 def test_bad_inputs_raise_value_error():
     # reference tests/test_f16acc.py:42-47 (runs here on CPU tensors: the device
     # check fires first for CPU operands, the shape check for mismatched K)

@@ -42,6 +42,23 @@ def oracle(a, b, out_dtype, cfg, chunked=True):
     return chunk32.mm(a, b, out_dtype, chunked=chunked, tile=(cfg["bm"], cfg["bn"]), return_flags=True)
 
 
+def assert_carries_chunk_rounding(c, ref, f32, K, what):
+    """An FP32 output c of the chunked kernel against the oracle's chunk sum
+    ref and plain FP32 accumulation f32 (no tile flagged).  For N(0, 1)
+    inputs every FP32 sum of fp16-rounded partials is exact, so c can only
+    differ from ref where one of its chunks' FP32 partials rounds to the
+    other fp16 neighbour in the MFMA than on the host (measured ~4e-4 of the
+    elements per chunk on MI355X); FP32 accumulation keeps almost no bits.
+    The max-norm error cannot tell the two apart (one such partial moves an
+    element as much as the chunk rounding moves the worst one), the L2 norm
+    and the bit count can."""
+    c, ref, f32 = c.float().cpu(), ref.float().cpu(), f32.float().cpu()
+    chunks = -(-K // 32)
+    same = float((c.view(torch.int32) == ref.view(torch.int32)).float().mean())
+    assert same > 1.0 - 1e-3 * chunks, (what, same)
+    assert float((c - ref).norm()) < 0.2 * float((f32 - ref).norm()), what
+
+
 ALL_TILES = ["256x256", "256x128", "128x256", "128x128", "generic", "64x64", "128x96k2", "64x32k4", "256x288"]
 
 
@@ -94,12 +111,15 @@ def test_full_size_square_gemms_match_oracle_and_fp64(n):
     # chunk) reproduces its published 4.8e-4 at 4096^3.  The kernel rounds each
     # chunk once, and stays within the 1e-3 budget of that model as well.
     s16 = chunk32.chunked_sum(a, b, mode="per_k16") if n == 4096 else None
+    f32 = chunk32.fp32_sum(a, b)
     ref64 = a.cuda().double() @ b.cuda().double()
     for b_t in (False, True):
         for out_dtype in (torch.float16, torch.float32):
             c, flags, cfg = run(a, b, out_dtype, b_transposed=b_t)
             assert cfg["tile"] == "256x256" and int(flags.sum()) == 0, (n, b_t, out_dtype, cfg)
             assert rel(c, s.to(out_dtype)) < TOL, (n, b_t, out_dtype)
+            if out_dtype == torch.float32:
+                assert_carries_chunk_rounding(c, s, f32, n, (n, b_t))
             if s16 is not None:
                 assert rel(c, s16.to(out_dtype)) < TOL, (n, b_t, out_dtype, "per_k16")
             assert rel(c.cuda(), ref64) < 5.1e-4, (n, b_t, out_dtype)
@@ -261,6 +281,8 @@ def test_every_tile_matches_oracle(tile, K):
             ref, rflags = oracle(a, b, out_dtype, cfg)
             assert torch.equal(flags.cpu(), rflags)
             assert rel(c.cpu(), ref) < TOL, (tile, K, b_t, out_dtype)
+            if out_dtype == torch.float32:
+                assert_carries_chunk_rounding(c, ref, a.float() @ b.float(), K, (tile, K, b_t))
         c32 = mm_tile(ga, gb, tile, torch.float32, chunked=False)
         assert rel(c32.cpu(), (a.float() @ b.float()).double()) < 1e-5
 
@@ -1077,7 +1099,15 @@ def test_graphs_captured_on_one_stream_get_their_own_split_k_workspaces():
 
 def _random_operand(g, rows, cols, kind, seed):
     """A [rows, cols] fp16 CPU tensor laid out as `kind` (its GPU twin has the
-    same strides): contiguous, transposed view, strided view or offset view."""
+    same strides): contiguous, transposed view, strided view, offset view,
+    broadcast view (one row or one column expanded: a stride of 0) or
+    sliding window (rows 8 elements apart, overlapping when cols > 8)."""
+    if kind == "broadcast":
+        if seed % 2:
+            return rnd((cols,), seed).expand(rows, cols)
+        return rnd((rows, 1), seed).expand(rows, cols)
+    if kind == "window":
+        return rnd((8 * max(rows - 1, 0) + cols,), seed).as_strided((rows, cols), (8, 1))
     n = 3 * max(rows, cols) + 5
     base = rnd((n, n), seed)
     if kind == "contiguous":
@@ -1092,7 +1122,8 @@ def _random_operand(g, rows, cols, kind, seed):
 @pytest.mark.parametrize("case", range(40))
 def test_randomized_shapes_layouts_and_tiles_match_oracle(case):
     """Seeded random problems: M, N in 1..300, K in 0..700 (ragged chunks and
-    stages), each operand contiguous / transposed / strided / offset, fp16 or
+    stages), each operand contiguous / transposed / strided / offset /
+    broadcast / sliding window, fp16 or
     fp32 output, chunked or not, the table's tile or a forced one; values and
     tile flags against the oracle, some tiles overflowing on purpose."""
     import random
@@ -1101,11 +1132,15 @@ def test_randomized_shapes_layouts_and_tiles_match_oracle(case):
 
     r = random.Random(1000 + case)
     M, N, K = r.randint(1, 300), r.randint(1, 300), r.choice([0, 1, 7, 32, 33, 64, 96, 200, r.randint(1, 700)])
-    kinds = ["contiguous", "transposed", "strided", "offset"]
-    a = _random_operand(None, M, K, r.choice(kinds), 2000 + case)
-    b = _random_operand(None, K, N, r.choice(kinds), 3000 + case)
+    kinds = ["contiguous", "transposed", "strided", "offset", "broadcast", "window"]
+    ka, kb = r.choice(kinds), r.choice(kinds)
+    a = _random_operand(None, M, K, ka, 2000 + case)
+    b = _random_operand(None, K, N, kb, 3000 + case)
     assert a.shape == (M, K) and b.shape == (K, N)
-    if K >= 64 and r.random() < 0.3:  # one overflowing block of rows x cols: chunk sums past 65504
+    # one overflowing block of rows x cols (chunk sums past 65504), written
+    # only into operands whose elements each have their own memory
+    disjoint = ka not in ("broadcast", "window") and kb not in ("broadcast", "window")
+    if K >= 64 and r.random() < 0.3 and disjoint:
         i0, j0 = r.randrange(M), r.randrange(N)
         a[i0 : i0 + 4, :] = 60.0
         b[:, j0 : j0 + 4] = 60.0

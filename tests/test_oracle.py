@@ -247,3 +247,25 @@ def test_reference_accuracy_figures_at_4096():
     once = rel(chunk32.mm(a, b), ref)
     assert 4.4e-4 < per16 < 5.2e-4
     assert 3.5e-4 < once <= per16
+
+
+@pytest.mark.parametrize("kgroups", [1, 2, 3, 4])
+def test_paired_sum_is_the_chunk_sum_reassociated(kgroups):
+    """paired_sum adds the same fp16-rounded chunk partials in another FP32
+    order (pairs of chunks, K ranges summed apart): equal to chunked_sum
+    wherever every sum is exact (small integers), and a dropped or doubled
+    chunk, a misplaced range or pairs across stage boundaries would break
+    that equality on these ragged K."""
+    g = torch.Generator().manual_seed(kgroups)
+    for K in (1, 31, 64, 65, 200, 333):
+        a = torch.randint(-3, 4, (9, K), generator=g).half()
+        b = torch.randint(-3, 4, (K, 7), generator=g).half()
+        want = chunk32.chunked_sum(a, b)
+        assert torch.equal(chunk32.paired_sum(a, b, kgroups), want), K
+        assert torch.equal(chunk32.paired_sum(a, b, kgroups, exact_partials=True), want), K
+    # a chunk that overflows fp16 in one range: inf, as in the chunk sum
+    a = torch.ones(2, 256, dtype=torch.float16)
+    b = torch.ones(256, 2, dtype=torch.float16)
+    b[200:232, 0] = 3000.0
+    assert torch.isinf(chunk32.paired_sum(a, b, kgroups)[:, 0]).all()
+    assert torch.equal(chunk32.paired_sum(a, b, kgroups)[:, 1], chunk32.chunked_sum(a, b)[:, 1])
