@@ -20,7 +20,9 @@ redo.  Prints one JSON line:
 Other workloads (--workload) are sweeps for the design record, not bench lines;
 --workload shapes reports every configured shape against hipBLASLt;
 --workload redo_overhead times the shipped kernels against a build without the
-overflow flag and redo on data that never overflows; --workload
+overflow flag and redo on data that never overflows; --workload persistent_ab
+times multi-round shapes on the persistent kernel against a build that runs
+them one tile per workgroup; --workload
 overflow_split_redo times the overflow stress workload against a build that
 redoes flagged tiles in a split-K pass instead of in the same workgroup;
 --workload table_check times the per-shape table against every forced tile on
@@ -522,27 +524,25 @@ REDO_SHAPES = (("gemm4096_f32", 4096, 4096, 4096, "row", torch.float32),
                ("qwen_down", 2048, 1536, 8960, "t", torch.float16))
 
 
-def redo_overhead(rounds=7):
-    """What the overflow flag and the in-kernel FP32 redo cost when no tile
-    overflows: f16acc_gemm_ws (the entry mm uses: split-K where the table
-    splits) of the shipped library against the same source built with both
-    compiled out (libf16acc_amd_noredo.so, -DF16ACC_NO_REDO=1, loaded here
-    only), called through the C ABI on the same inputs, timed in interleaved
-    settled bursts (median over rounds).  Both must return the same bits on
-    this data (no tile overflows).  The reference calls an in-kernel redo 8 %
-    slower and a separate one "nearly free" (f16acc/kernel.py:6-9,
-    README.md:20)."""
+def twin_ab(lib_path, shapes, rounds, shipped="shipped", twin="twin"):
+    """f16acc_gemm_ws (the entry mm uses: split-K where the table splits) of
+    the shipped library against the same source built with a -D switch
+    (lib_path, loaded here only), through the C ABI on the same inputs, timed
+    in interleaved settled bursts (median over rounds); both return the same
+    bits on these inputs.  Yields one record per shape."""
     import ctypes
 
-    from f16acc_amd import _lib, build
+    from f16acc_amd import _lib
 
-    noredo = ctypes.CDLL(build.LIB_NOREDO)
-    gemm_noredo = noredo.f16acc_gemm_ws
-    gemm_noredo.argtypes, gemm_noredo.restype = _lib.gemm_ws.argtypes, _lib.gemm_ws.restype
-    ws = torch.empty(32 << 20, dtype=torch.uint8, device="cuda")  # every split on 256 CUs fits
-    for name, M, N, K, layout, out_dtype in REDO_SHAPES:
+    other = ctypes.CDLL(lib_path)
+    gemm_other = other.f16acc_gemm_ws
+    gemm_other.argtypes, gemm_other.restype = _lib.gemm_ws.argtypes, _lib.gemm_ws.restype
+    # every split on 256 CUs fits; the header (deferred redo list) starts empty
+    ws = torch.empty((32 << 20) + _lib.WS_HEADER, dtype=torch.uint8, device="cuda")
+    ws[:_lib.WS_HEADER].zero_()
+    for name, M, N, K, layout, out_dtype in shapes:
         _, _, a, b = make_inputs(M, N, K, layout)
-        outs = {k: torch.empty(M, N, device="cuda", dtype=out_dtype) for k in ("shipped", "no_redo")}
+        outs = {k: torch.empty(M, N, device="cuda", dtype=out_dtype) for k in (shipped, twin)}
         stream = torch.cuda.current_stream().cuda_stream
         code = _lib.OUT_F32 if out_dtype == torch.float32 else _lib.OUT_F16
 
@@ -551,26 +551,58 @@ def redo_overhead(rounds=7):
                                          a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1), code, 1,
                                          stream, ws.data_ptr(), ws.numel()))
 
-        ops = {"shipped": call(_lib.gemm_ws, outs["shipped"]), "no_redo": call(gemm_noredo, outs["no_redo"])}
+        ops = {shipped: call(_lib.gemm_ws, outs[shipped]), twin: call(gemm_other, outs[twin])}
         for op in ops.values():
             op()
         torch.cuda.synchronize()
-        same = bool(torch.equal(outs["shipped"], outs["no_redo"]))
+        same = bool(torch.equal(outs[shipped], outs[twin]))
         times = {k: [] for k in ops}
         for _ in range(rounds):
             for k, op in ops.items():
                 times[k].append(settled_time(op))
         t = {k: statistics.median(v) for k, v in times.items()}
-        print(json.dumps({"workload": name, "M": M, "N": N, "K": K,
-                          "b": "row-major [K,N]" if layout == "row" else "w.t()",
-                          "out": "fp32" if out_dtype == torch.float32 else "fp16",
-                          "us_shipped": round(t["shipped"] * 1e6, 2), "us_no_redo": round(t["no_redo"] * 1e6, 2),
-                          "redo_overhead_pct": round((t["shipped"] / t["no_redo"] - 1) * 100, 2),
-                          "per_round_pct": [round((x / y - 1) * 100, 2) for x, y in zip(times["shipped"],
-                                                                                        times["no_redo"])],
-                          "same_bits": same, "rounds": rounds}), flush=True)
+        yield {"workload": name, "M": M, "N": N, "K": K, "b": "row-major [K,N]" if layout == "row" else "w.t()",
+               "out": "fp32" if out_dtype == torch.float32 else "fp16",
+               f"us_{shipped}": round(t[shipped] * 1e6, 2), f"us_{twin}": round(t[twin] * 1e6, 2),
+               "tflops": round(2 * M * N * K / t[shipped] / 1e12, 1),
+               "pct": round((t[shipped] / t[twin] - 1) * 100, 2),
+               "per_round_pct": [round((x / y - 1) * 100, 2) for x, y in zip(times[shipped], times[twin])],
+               "same_bits": same, "rounds": rounds}
         del a, b, outs
         torch.cuda.empty_cache()
+
+
+def redo_overhead(rounds=7):
+    """What the overflow flag and the in-kernel FP32 redo cost when no tile
+    overflows: the shipped library against the same source built with both
+    compiled out (libf16acc_amd_noredo.so, -DF16ACC_NO_REDO=1).  Both must
+    return the same bits on this data (no tile overflows).  The reference
+    calls an in-kernel redo 8 % slower and a separate one "nearly free"
+    (f16acc/kernel.py:6-9, README.md:20)."""
+    from f16acc_amd import build
+
+    for rec in twin_ab(build.LIB_NOREDO, REDO_SHAPES, rounds, twin="no_redo"):
+        rec["redo_overhead_pct"] = rec.pop("pct")
+        print(json.dumps(rec), flush=True)
+
+
+PERSISTENT_SHAPES = (("qwen_lm_head", 2048, 151936, 1536, "t", torch.float16),
+                     ("gemm8192", 8192, 8192, 8192, "row", torch.float16),
+                     ("gemm8192_bt", 8192, 8192, 8192, "t", torch.float16),
+                     ("gemm8192_f32", 8192, 8192, 8192, "row", torch.float32),
+                     ("llama3_gateup_4096tok", 4096, 14336, 4096, "t", torch.float16),
+                     ("llama2_lm_head_4096tok", 4096, 32000, 4096, "t", torch.float16))
+
+
+def persistent_ab(rounds=5):
+    """Multi-round shapes on the persistent 256x256 kernel (the shipped
+    library) against the one-tile-per-workgroup grid
+    (libf16acc_amd_nopersist.so, -DF16ACC_NO_PERSISTENT=1): pct < 0 means the
+    persistent kernel is faster."""
+    from f16acc_amd import build
+
+    for rec in twin_ab(build.LIB_NOPERSIST, PERSISTENT_SHAPES, rounds, twin="grid"):
+        print(json.dumps(rec), flush=True)
 
 
 def qwen2_model(layers=28, seed=0, dtype=torch.float16):
@@ -668,7 +700,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="gemm4096",
                     choices=sorted(WORKLOADS) + ["copy", "overflow", "overflow_split_redo", "qwen2_prefill",
-                                                 "redo_overhead", "shapes",
+                                                 "redo_overhead", "persistent_ab", "shapes",
                                                  "table_check"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and oracle comparison")
     ap.add_argument("--preheat", type=float, default=PREHEAT_S,
@@ -698,6 +730,8 @@ def main():
         return overflow_split_redo()
     if args.workload == "redo_overhead":
         return redo_overhead()
+    if args.workload == "persistent_ab":
+        return persistent_ab()
     if args.workload == "qwen2_prefill":
         line = {"workload": "random-init Qwen2.5-1.5B FP16 prefill, batch 1, 2048 seeded tokens",
                 **qwen2_prefill_ab()}

@@ -73,9 +73,10 @@ abi_version.restype = _int
 # Exported symbol names, as declared in include/f16acc.h.
 EXPORTS = ("f16acc_gemm", "f16acc_gemm_bias", "f16acc_gemm_ws", "f16acc_gemm_noalloc", "f16acc_workspace_size", "f16acc_gemm_tile", "f16acc_gemm_tile_ws", "f16acc_pack", "f16acc_tile_config", "f16acc_block_tile", "f16acc_strerror",
            "f16acc_abi_version", "f16acc_tail_split")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 OUT_F16, OUT_F32 = 0, 1
+WS_HEADER = 4096  # F16ACC_WS_HEADER: the first bytes of a workspace, zero on first use
 E_ARG, E_UNSUPPORTED, E_SCRATCH, E_DEVICE = -1, -2, -3, -4
 TILES = ("256x256", "256x128", "128x256", "128x128", "generic", "64x64", "128x96k2", "64x32k4",
          "256x288")  # F16ACC_TILE_* ids

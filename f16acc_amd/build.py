@@ -25,6 +25,10 @@ LIB_NOREDO = os.path.join(OUT_DIR, "libf16acc_amd_noredo.so")
 # ... and with the split redo in place of the in-kernel one for 256x256
 # (-DF16ACC_SPLIT_REDO=1): only bench.py's overflow workload loads it.
 LIB_SPLITREDO = os.path.join(OUT_DIR, "libf16acc_amd_splitredo.so")
+# ... and with multi-round shapes on the one-tile-per-workgroup grid instead
+# of the persistent kernel (-DF16ACC_NO_PERSISTENT=1): only bench.py's
+# persistent A/B loads it.
+LIB_NOPERSIST = os.path.join(OUT_DIR, "libf16acc_amd_nopersist.so")
 CHUNKRATE = os.path.join(OUT_DIR, "chunkrate")  # MFMA / chunk-epilogue microbenchmark
 ARCH = "gfx950"
 
@@ -71,10 +75,11 @@ def _finish(job, verbose):
 
 
 def build(verbose=False):
-    """Compile the library, its no-redo and split-redo twins and the
-    chunkrate microbenchmark (four hipcc processes at once)."""
+    """Compile the library, its no-redo, split-redo and no-persistent twins
+    and the chunkrate microbenchmark (five hipcc processes at once)."""
     jobs = [_start(HIP_FLAGS, SRC, LIB), _start(HIP_FLAGS + ["-DF16ACC_NO_REDO=1"], SRC, LIB_NOREDO),
             _start(HIP_FLAGS + ["-DF16ACC_SPLIT_REDO=1"], SRC, LIB_SPLITREDO),
+            _start(HIP_FLAGS + ["-DF16ACC_NO_PERSISTENT=1"], SRC, LIB_NOPERSIST),
             _start(COMMON_FLAGS, CHUNKRATE_SRC, CHUNKRATE)]
     errors = []
     for job in jobs:

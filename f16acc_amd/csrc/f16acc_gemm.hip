@@ -92,7 +92,45 @@ constexpr bool kRedo = !F16ACC_NO_REDO;
 #endif
 constexpr bool kSplitRedo = F16ACC_SPLIT_REDO && kRedo;
 
+// F16ACC_NO_PERSISTENT=1 runs multi-round shapes on the one-tile-per-
+// workgroup grid instead of the persistent kernel (gemm_persistent); only
+// the benchmark's A/B of the two builds loads it (same bits either way).
+#ifndef F16ACC_NO_PERSISTENT
+#define F16ACC_NO_PERSISTENT 0
+#endif
+constexpr bool kPersistent = !F16ACC_NO_PERSISTENT;
+
 static_assert(kStageK == 2 * kChunk, "a stage holds exactly one chunk pair");
+
+// Deferred redo list, the first F16ACC_WS_HEADER bytes of a caller's
+// workspace (zero when first used; left zero by every call): the chunked
+// launch appends each flagged tile's id, the redo launch that follows
+// recomputes those tiles, and its last workgroup empties the list again.
+// The redo launch's workgroups count themselves done on kDoneLines counters,
+// each on its own 128-byte line (device-scope atomics on one address
+// serialise: one counter for 512 workgroups cost ~9 us a call), and the last
+// workgroup of each counter on one more.
+constexpr int kDoneLines = 8;
+struct RedoList {
+  int count;  // tiles appended (an atomic counter)
+  int pad0[31];
+  int groups_done;  // counters whose workgroups have all finished
+  int pad1[31];
+  struct {
+    int n;
+    int pad[31];
+  } done[kDoneLines];  // finished workgroups with blockIdx.x % kDoneLines == j
+  int items[(F16ACC_WS_HEADER - 128 * (2 + kDoneLines)) / 4];
+};
+constexpr int kRedoMax = (F16ACC_WS_HEADER - 128 * (2 + kDoneLines)) / 4;
+static_assert(sizeof(RedoList) == F16ACC_WS_HEADER, "the list fills the workspace header");
+
+__device__ __forceinline__ int load_agent(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 struct Params {
   const f16* a;
@@ -121,6 +159,9 @@ struct Params {
   const uint8_t* redo_only;
   int64_t redo_tn;
   int redo_sh;
+  // deferred redo (whole-K chunked launch): flagged tiles are appended here
+  // instead of being redone by their workgroup (NULL: redo in place)
+  RedoList* list;
 };
 
 enum Mode { kWhole = 0, kPartial = 1, kFinish = 2 };
@@ -799,18 +840,33 @@ __device__ __forceinline__ void group_reduce(char LDS_AS* smem, int g, int ltid,
 // shape.  (FP32 accumulation keeps k_loop_fast: there this form ran 2-6 %
 // slower.)
 
-template <class C>
+//
+// entry (the persistent kernel's tile chaining): kIssueFirst, the loop
+// issues stage 0's copies itself; kFirstThenStores, they were issued before
+// exactly STORES more vector memory instructions of this wave (a tile's
+// output stores), so waiting until STORES remain outstanding has them
+// landed (vmcnt counts in issue order) while the stores drain; kFirstIssued,
+// issued before an unknown number of others: wait for everything.
+enum Entry { kIssueFirst = 0, kFirstThenStores = 1, kFirstIssued = 2 };
+
+template <class C, int STORES = 0>
 __device__ __forceinline__ void k_loop_cross(const Params& p, int64_t m0, int64_t n0, int64_t kbeg, int64_t kend,
                                              char LDS_AS* smem, FastLoader<C>& ld, int wave, int wm, int wn, int lane,
-                                             f32x4 (&acc)[C::FM][C::FN]) {
+                                             f32x4 (&acc)[C::FM][C::FN], int entry = kIssueFirst) {
   constexpr int T = C::FM * C::FN, kUnits = C::LA + C::LB;
   static_assert(kUnits <= T - C::FM, "copies must go out before the last column");
   static_assert(C::NS == 2 && C::KG == 1 && C::FM > 1, "two-stage ring, one K group");
   const int64_t nsteps = kend > kbeg ? (kend - kbeg + kStageK - 1) / kStageK : 0;
-  if (nsteps <= 0) return;
+  if (nsteps <= 0) {
+    if (entry != kIssueFirst) wait_vm0();  // a prefetched stage (zeros past K) must land before the LDS is reused
+    return;
+  }
   const int r16 = lane & 15, g = lane >> 4;
-  ld.issue(p, m0, n0, kbeg, kend, smem, wave);
-  wait_vm0();
+  if (entry == kIssueFirst) ld.issue(p, m0, n0, kbeg, kend, smem, wave);
+  if (entry == kFirstThenStores)
+    wait_vm<STORES>();
+  else
+    wait_vm0();
   __syncthreads();
   f16x8 af[C::FM][2], bc[2], bn[2];
   bc[0] = read_b<C>(smem + C::A_STAGE, wn, 0, 0, lane);
@@ -1107,57 +1163,67 @@ __device__ __forceinline__ int stg_swz(int u, int row) {
 // which reached HBM as partial lines (about twice the output's bytes
 // written, by rocprofv3 WRITE_SIZE).  Each wave stages its own WTM x WTN
 // sub-tile in its own LDS slice (the LDS is free once the K loop's final
-// barrier has passed), 16-byte units XOR-swizzled by row.  Needs rows of c
+// barrier has passed), 16-byte units XOR-swizzled by row, in P passes of
+// FN / P column blocks (a wave's LDS operations run in order, so a pass's
+// writes never overtake the previous pass's reads).  Needs rows of c
 // contiguous (scn == 1).  Rows that are not 16-byte aligned (N = 1537) take
 // 16-byte stores at their 2-byte aligned addresses, and units at the edge
 // of c are stored element by element, so edge tiles and odd N stay on this
-// path instead of one 2-byte store per element and lane.
-template <class C>
+// path instead of one 2-byte store per element and lane.  A wave whose
+// sub-tile is whole issues exactly P * WTM * (2 FN / P) / 64 stores.
+template <class C, int P = 1>
 __device__ __forceinline__ void store_tile_staged(const Params& p, int64_t m0, int64_t n0, int wm, int wn, int lane,
                                                   int wave, char LDS_AS* smem, const f32x4 (&acc)[C::FM][C::FN]) {
   typedef f16 f16x4 __attribute__((ext_vector_type(4)));
-  constexpr int U = C::WTN / 8;  // 16-byte units per row of the wave tile
-  constexpr int ROW = C::WTN * 2;
+  static_assert(C::FN % P == 0, "passes split the column blocks evenly");
+  constexpr int FNP = C::FN / P;  // column blocks per pass
+  constexpr int U = 2 * FNP;      // 16-byte units per staged row
+  constexpr int ROW = U * 16;
   char LDS_AS* w = smem + wave * (C::WTM * ROW);
   const int r16 = lane & 15, g = lane >> 4;
   const int64_t col0 = n0 + wn * C::WTN;
-#pragma unroll
-  for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-    for (int j = 0; j < C::FN; ++j) {
-      const int row = 16 * i + r16, u = 2 * j + (g >> 1);
-      f32x4 v = acc[i][j];
-      if (p.bias) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t col = col0 + 16 * j + 4 * g + r;
-          if (col < p.N) v[r] = with_bias<false>(v[r], p.bias, col);
-        }
-      }
-      const f32x2 lo = {v[0], v[1]}, hi = {v[2], v[3]};
-      const f16x2 hl = __builtin_convertvector(lo, f16x2), hh = __builtin_convertvector(hi, f16x2);
-      const f16x4 o = {hl[0], hl[1], hh[0], hh[1]};
-      *(f16x4 LDS_AS*)(w + row * ROW + (stg_swz<U>(u, row) << 4) + (g & 1) * 8) = o;
-    }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
-  __builtin_amdgcn_wave_barrier();
   f16* cbase = (f16*)p.c + (m0 + wm * C::WTM) * p.scm + col0;
   const int64_t rows_in = p.M - (m0 + wm * C::WTM), cols_in = p.N - col0;  // of this wave's sub-tile
   const bool whole = p.vec_store && rows_in >= C::WTM && cols_in >= C::WTN;
 #pragma unroll
-  for (int it = 0; it < C::WTM * U / 64; ++it) {
-    const int idx = it * 64 + lane, row = idx / U, u = idx % U;
-    const f16x8 v = *(const f16x8 LDS_AS*)(w + row * ROW + (stg_swz<U>(u, row) << 4));
-    if (whole) {
-      *(f16x8*)(cbase + row * p.scm + 8 * u) = v;
-    } else if (row < rows_in) {
-      f16* dst = cbase + row * p.scm + 8 * u;
-      if (8 * u + 8 <= cols_in) {
-        *(f16x8_a2*)dst = v;
-      } else {
+  for (int pass = 0; pass < P; ++pass) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (8 * u + e < cols_in) dst[e] = v[e];
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+      for (int jj = 0; jj < FNP; ++jj) {
+        const int j = pass * FNP + jj;
+        const int row = 16 * i + r16, u = 2 * jj + (g >> 1);
+        f32x4 v = acc[i][j];
+        if (p.bias) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t col = col0 + 16 * j + 4 * g + r;
+            if (col < p.N) v[r] = with_bias<false>(v[r], p.bias, col);
+          }
+        }
+        const f32x2 lo = {v[0], v[1]}, hi = {v[2], v[3]};
+        const f16x2 hl = __builtin_convertvector(lo, f16x2), hh = __builtin_convertvector(hi, f16x2);
+        const f16x4 o = {hl[0], hl[1], hh[0], hh[1]};
+        *(f16x4 LDS_AS*)(w + row * ROW + (stg_swz<U>(u, row) << 4) + (g & 1) * 8) = o;
+      }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int it = 0; it < C::WTM * U / 64; ++it) {
+      const int idx = it * 64 + lane, row = idx / U, u = idx % U;
+      const int c = pass * FNP * 16 + 8 * u;  // column inside the wave's sub-tile
+      const f16x8 v = *(const f16x8 LDS_AS*)(w + row * ROW + (stg_swz<U>(u, row) << 4));
+      if (whole) {
+        *(f16x8*)(cbase + row * p.scm + c) = v;
+      } else if (row < rows_in) {
+        f16* dst = cbase + row * p.scm + c;
+        if (c + 8 <= cols_in) {
+          *(f16x8_a2*)dst = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (c + e < cols_in) dst[e] = v[e];
+        }
       }
     }
   }
@@ -1361,6 +1427,20 @@ __device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, 
     const int flag = tf.set_and_read(bad, lane);
     if (p.flags && tid == 0) p.flags[tm * p.tiles_n + tn] = (uint8_t)flag;
     if (__builtin_expect(!flag, 1) || (kSplitRedo && p.defer_redo)) return;
+    if (p.list) {
+      // deferred: the redo launch that follows recomputes this tile; a list
+      // that is full (or not zeroed) leaves the redo here.  The flag word
+      // carries the outcome once every wave has read the flag.
+      __syncthreads();
+      if (tid == 0) {
+        const int idx = atomicAdd(&p.list->count, 1);
+        const bool listed = idx >= 0 && idx < kRedoMax;
+        if (listed) store_agent(&p.list->items[idx], (int)(tm * p.tiles_n + tn));
+        *tf.word = listed ? 2 : 1;
+      }
+      __syncthreads();
+      if (*tf.word == 2) return;
+    }
     // redo the whole tile, all of K, with FP32 accumulation (kernel.py:75-81)
 #pragma unroll
     for (int i = 0; i < C::FM; ++i)
@@ -1374,6 +1454,174 @@ __device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, 
       k_loop_generic<C, false>(p, m0, n0, smem, tid, wm, wn, lane, acc);
   }
   if (g == 0) store_any<C, OUT32, SMEM>(p, smem, m0, n0, lw, wm, wn, lane, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Persistent chunked kernel for the 64x128-per-wave tiles (the table sends
+// 256x256 to it) on shapes of more than one round of tiles (the Qwen2.5-1.5B lm_head,
+// 2048 x 151936 x 1536: 18.6 rounds; 8192^3: 4).  One workgroup per CU
+// walks the tiles blockIdx.x, blockIdx.x + G, ... (G = gridDim.x, a multiple
+// of the 8 XCDs, so a workgroup keeps its XCD and round r runs the tiles a
+// one-tile-per-workgroup grid would run in its r-th round, in the same
+// block -> tile order).  At a tile's end the workgroup flags it (one
+// barrier), redoes it in FP32 if flagged (kernel.py:70-81), and then issues
+// the next tile's first-stage copies into ring slot 0 *before* staging and
+// storing this tile through the rest of the LDS: the next tile's first wait
+// covers those copies only (vmcnt counts in issue order, and exactly STORES
+// stores follow them in a wave with a whole sub-tile), so the stores drain
+// while the next tile's first stage is multiplied, and no workgroup launch,
+// prologue address setup or first-copy latency sits between tiles.
+// ---------------------------------------------------------------------------
+template <class C, bool OUT32>
+struct PersistentStore {
+  // the staging area: ring slot 1 onwards
+  static constexpr int AREA = C::RINGS - C::STAGE;
+  static constexpr int NW = C::WAVES_M * C::WAVES_N;
+  // fp16: the fewest column passes whose slices fit the area
+  static constexpr int P16 = passes(C::FN, (NW * C::WTM * C::WTN * 2 + AREA - 1) / AREA);
+  static constexpr int STORES16 = P16 * (C::WTM * (2 * C::FN / P16) / 64);
+  // fp32 (store_tile_staged32 with SMEM = AREA)
+  static constexpr int P32 = passes(C::FN, (NW * C::WTM * C::WTN * 4 + AREA - 1) / AREA);
+  static constexpr int STORES32 = P32 * (C::WTM * (C::WTN / P32 / 4) / 64);
+  static constexpr int STORES = OUT32 ? STORES32 : STORES16;
+  static_assert(STORES <= 63, "the stores must fit vmcnt");
+  static_assert(NW * C::WTM * (2 * C::WTN / P16) <= AREA, "fp16 staging slices must fit");
+  __device__ static __forceinline__ void store(const Params& p, char LDS_AS* area, int64_t m0, int64_t n0, int wave,
+                                               int wm, int wn, int lane, const f32x4 (&acc)[C::FM][C::FN]) {
+    if constexpr (OUT32)
+      store_tile_staged32<C, AREA>(p, m0, n0, wm, wn, lane, wave, area, acc);
+    else
+      store_tile_staged<C, P16>(p, m0, n0, wm, wn, lane, wave, area, acc);
+  }
+};
+
+template <class C, bool OUT32>
+__global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) void gemm_persistent(Params p) {
+  static_assert(C::KG == 1 && C::NS == 2 && C::FM * C::FN >= 32, "the chunked 64x128-per-wave tiles");
+  using PS = PersistentStore<C, OUT32>;
+  __shared__ __attribute__((aligned(1024))) char smem_raw[C::RINGS];
+  __shared__ int flag_word[2];  // tile i raises word i & 1; the other is cleared meanwhile
+  char LDS_AS* smem = (char LDS_AS*)smem_raw;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+  const int64_t tiles = p.tiles_m * p.tiles_n, G = gridDim.x;
+  int64_t t = blockIdx.x;
+  if (t >= tiles) return;
+  if (tid == 0) flag_word[0] = flag_word[1] = 0;  // ordered before any raise by the K loop's barriers
+  int64_t tm, tn;
+  group_m(xcd_order(t, tiles), p.tiles_m, p.tiles_n, &tm, &tn);
+  int entry = kIssueFirst;
+  for (int it = 0;; ++it) {
+    const int64_t m0 = tm * C::BM, n0 = tn * C::BN;
+    // The lane's index, opaque to the compiler once per tile: every
+    // lane-dependent address (LDS fragments, copies, staged stores) is then
+    // computed inside the tile loop instead of hoisted out of it and kept
+    // live across the K loop, where the registers are all taken (hoisted,
+    // they spilled around every tile).
+    int tid_t = tid;
+    asm volatile("" : "+v"(tid_t));
+    const int lane_t = tid_t & 63;
+    FastLoader<C> ld;
+    ld.init(p, m0, n0, tid_t);
+    f32x4 acc[C::FM][C::FN];
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    k_loop_cross<C, PS::STORES>(p, m0, n0, 0, p.K, smem, ld, wave, wm, wn, lane_t, acc, entry);
+    if constexpr (kRedo) {
+      // tile flag: any element of the FP32 sum inf or NaN (kernel.py:70-71)
+      int LDS_AS* word = (int LDS_AS*)&flag_word[it & 1];
+      bool bad = false;
+#pragma unroll
+      for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) bad |= !(__builtin_fabsf(acc[i][j][r]) < __builtin_inff());
+      if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane_t == 0) *word = 1;
+      __syncthreads();
+      const int flag = *word;
+      // the other word's last reads were a tile ago; its next raise comes
+      // after the next tile's barriers
+      if (tid_t == 0) flag_word[(it + 1) & 1] = 0;
+      if (p.flags && tid_t == 0) p.flags[tm * p.tiles_n + tn] = (uint8_t)flag;
+      if (__builtin_expect(flag, 0)) {
+        // redo the whole tile, all of K, with FP32 accumulation (kernel.py:75-81)
+#pragma unroll
+        for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+          for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        k_loop_fast<C, false>(p, m0, n0, 0, p.K, smem, ld, wave, wm, wn, lane_t, acc);
+      }
+    }
+    t += G;
+    const bool next = t < tiles;
+    if (next) {
+      group_m(xcd_order(t, tiles), p.tiles_m, p.tiles_n, &tm, &tn);
+      FastLoader<C> nld;
+      nld.init(p, tm * C::BM, tn * C::BN, tid_t);
+      nld.issue(p, tm * C::BM, tn * C::BN, 0, p.K, smem, wave);  // into slot 0, free since the last barrier
+    }
+    PS::store(p, smem + C::STAGE, m0, n0, wave, wm, wn, lane_t, acc);
+    if (!next) return;
+    const int64_t rows_in = p.M - (m0 + wm * C::WTM), cols_in = p.N - (n0 + wn * C::WTN);
+    const bool whole = p.vec_store && rows_in >= C::WTM && cols_in >= C::WTN && !p.bias && !p.flags;
+    entry = whole ? kFirstThenStores : kFirstIssued;
+    __syncthreads();  // every wave's staging reads done: the next stage's copies may overwrite slot 1
+  }
+}
+
+// The redo launch of the deferred list (RedoList): the tiles a chunked
+// 256x256 launch flagged, each recomputed whole with FP32 accumulation
+// (kernel.py:75-81) as its four 128x128 quarters by four workgroups of C
+// (128x128, the chunked launch's b layout), over all of K in order: each
+// element sums exactly what the in-place redo sums, in the same order (same
+// bits).  p.tiles_n is the 256x256 grid's.  Every workgroup leaves at once
+// when the list is empty; the last to finish empties it for the next call
+// (all have read the count by then: each reads it before counting itself
+// done, on the RedoList counters).
+template <class C, bool OUT32>
+__global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) void redo_list_kernel(Params p) {
+  static_assert(C::BM == 128 && C::BN == 128 && C::KG == 1, "quarters of 256x256 tiles");
+  constexpr int kSmem = C::RINGS > C::BM * C::BN * 2 ? C::RINGS : C::BM * C::BN * 2;
+  __shared__ __attribute__((aligned(1024))) char smem_raw[kSmem];
+  char LDS_AS* smem = (char LDS_AS*)smem_raw;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
+  int count = __builtin_amdgcn_readfirstlane(load_agent(&p.list->count));
+  count = count < 0 ? 0 : count > kRedoMax ? kRedoMax : count;
+  const int64_t tiles = p.tiles_m * p.tiles_n;
+  for (int64_t item = blockIdx.x; item < 4 * (int64_t)count; item += gridDim.x) {
+    const int tile = __builtin_amdgcn_readfirstlane(load_agent(&p.list->items[item >> 2]));
+    if (tile < 0 || tile >= tiles) continue;
+    const int64_t m0 = (2 * (tile / p.tiles_n) + ((item >> 1) & 1)) * 128;
+    const int64_t n0 = (2 * (tile % p.tiles_n) + (item & 1)) * 128;
+    if (m0 >= p.M || n0 >= p.N) continue;
+    f32x4 acc[C::FM][C::FN];
+#pragma unroll
+    for (int i = 0; i < C::FM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    FastLoader<C> ld;
+    ld.init(p, m0, n0, tid);
+    k_loop_fast<C, false>(p, m0, n0, 0, p.K, smem, ld, wave, wm, wn, lane, acc);
+    store_any<C, OUT32, kSmem>(p, smem, m0, n0, wave, wm, wn, lane, acc);
+    __syncthreads();  // staging reads done before the next quarter's copies
+  }
+  if (tid == 0) {
+    const int G = (int)gridDim.x, j = (int)(blockIdx.x % kDoneLines);
+    const int members = (G - j + kDoneLines - 1) / kDoneLines, lines = G < kDoneLines ? G : kDoneLines;
+    if (atomicAdd(&p.list->done[j].n, 1) == members - 1) {
+      store_agent(&p.list->done[j].n, 0);
+      if (atomicAdd(&p.list->groups_done, 1) == lines - 1) {
+        store_agent(&p.list->count, 0);
+        store_agent(&p.list->groups_done, 0);
+      }
+    }
+  }
 }
 
 // FP32 partials of a split tile, thread-private order: split s, block
@@ -1923,6 +2171,24 @@ hipError_t launch_fast(const Params& p, int blayout, int out32, int chunked, hip
                         : launch_cfg<CF<kNC>, LD>(p, out32, chunked, st);
 }
 
+template <class C>
+hipError_t launch_persistent(const Params& p, int out32, int grid, hipStream_t st) {
+  if (out32)
+    hipLaunchKernelGGL((gemm_persistent<C, true>), dim3((unsigned)grid), dim3(C::T), 0, st, p);
+  else
+    hipLaunchKernelGGL((gemm_persistent<C, false>), dim3((unsigned)grid), dim3(C::T), 0, st, p);
+  return hipGetLastError();
+}
+
+template <class C>
+hipError_t launch_redo_list(const Params& p, int out32, int grid, hipStream_t st) {
+  if (out32)
+    hipLaunchKernelGGL((redo_list_kernel<C, true>), dim3((unsigned)grid), dim3(C::T), 0, st, p);
+  else
+    hipLaunchKernelGGL((redo_list_kernel<C, false>), dim3((unsigned)grid), dim3(C::T), 0, st, p);
+  return hipGetLastError();
+}
+
 template <template <int> class CF>
 hipError_t launch_finish(const Params& p, int out32, int chunked, hipStream_t st) {
   using C = CF<kKC>;
@@ -1975,6 +2241,21 @@ inline SplitPlan plan_split(const Choice& ch, int64_t M, int64_t N, int64_t K, i
   return sp;
 }
 
+// Deferred redo: a whole-K chunked launch of at most one round of 256x256
+// tiles lists its flagged tiles in the workspace header instead of redoing
+// them in place, and a second launch recomputes them four workgroups a tile
+// (redo_list_kernel, one workgroup per CU).  In place, a flagged tile's workgroup runs a whole
+// FP32 K loop after the others have finished: on the overflow stress
+// workload (4096^3, 49 of 256 tiles flagged) it ran 222.7 us against 150.2
+// for the same shape clean.  Multi-round shapes keep the in-place redo (the
+// other workgroups go on with the next tiles meanwhile).
+inline bool deferred_redo(const Choice& ch, int64_t M, int64_t N, int64_t K, int cus) {
+  if (!kRedo || kSplitRedo || ch.family != F16ACC_FAMILY_FAST || ch.tile != F16ACC_TILE_256x256 || K <= 0)
+    return false;
+  const int64_t tiles = cdiv(M, 256) * cdiv(N, 256);
+  return tiles <= cus && tiles <= kRedoMax;
+}
+
 // Split redo (F16ACC_SPLIT_REDO builds only, for the benchmark): the
 // flagged 256x256 tiles of a chunked launch recomputed with FP32
 // accumulation as 2 x 2 tiles of 128x128, each over three K ranges, then
@@ -2015,6 +2296,7 @@ inline int split_redo(const Params& p, float* ws, int blayout, int out32, hipStr
   q.splits = (int)cdiv(nsteps, per);
   q.kps = per * kStageK;
   q.ws = ws;
+  q.list = nullptr;
   q.mode = kPartial;
   int rc = (int)launch_fast<Cfg3>(q, blayout, out32, 0, st);
   if (rc != 0) return rc;
@@ -2047,7 +2329,7 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
       const Choice tc = tp.rows ? choose(M - at, N, K, sam, sak, sbk, sbn, (const f16*)a + at * sam, b, -1, false)
                                 : choose(M, N - at, K, sam, sak, sbk, sbn, a, (const f16*)b + at * sbn, -1, false);
       const SplitPlan ts = tp.rows ? plan_split(tc, M - at, N, K, cu_count()) : plan_split(tc, M, N - at, K, cu_count());
-      if (ts.bytes > ws_bytes) return F16ACC_E_SCRATCH;
+      if (ws_bytes < F16ACC_WS_HEADER || ts.bytes > ws_bytes - F16ACC_WS_HEADER) return F16ACC_E_SCRATCH;
     }
     if (tp.rows) {
       const int rc = gemm_impl(a, b, bias, c, nullptr, at, N, K, sam, sak, sbk, sbn, scm, scn, out_dtype, chunked,
@@ -2086,15 +2368,22 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
   p.redo_only = nullptr;
   p.redo_tn = 0;
   p.redo_sh = 0;
-  if (workspace) {
+  p.list = nullptr;
+  // A workspace starts with the deferred redo list (F16ACC_WS_HEADER bytes);
+  // split-K partials follow it.
+  const bool has_ws = workspace && ws_bytes >= F16ACC_WS_HEADER;
+  if (strict_ws && !has_ws) return F16ACC_E_SCRATCH;
+  if (has_ws) {
     const SplitPlan sp = plan_split(ch, M, N, K, cu_count());
-    if (strict_ws && sp.bytes > ws_bytes) return F16ACC_E_SCRATCH;
-    if (sp.splits > 1 && ws_bytes >= sp.bytes) {
+    const size_t split_bytes = ws_bytes - F16ACC_WS_HEADER;
+    if (strict_ws && sp.bytes > split_bytes) return F16ACC_E_SCRATCH;
+    if (sp.splits > 1 && split_bytes >= sp.bytes) {
       p.mode = kPartial;
       p.splits = sp.splits;
       p.kps = sp.kps;
-      p.ws = (float*)workspace;
+      p.ws = (float*)((char*)workspace + F16ACC_WS_HEADER);
     }
+    if (chunked && deferred_redo(ch, M, N, K, cu_count()) && p.mode == kWhole) p.list = (RedoList*)workspace;
   }
   if (p.tiles_m * p.tiles_n * p.splits > 0x7fffffff) return F16ACC_E_UNSUPPORTED;
   const int out32 = out_dtype == F16ACC_OUT_F32;
@@ -2123,8 +2412,29 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
     if (!p.flags) p.flags = split_redo_flags();
     p.defer_redo = p.flags != nullptr;
   }
+  // Shapes of more than one round of 256x256 tiles, chunked, with
+  // contiguous output rows: one persistent workgroup per CU walks the tiles
+  // (gemm_persistent), chaining each tile's first copies ahead of the
+  // previous tile's store.  (256x288 keeps the grid: its persistent kernel
+  // spills a few registers per tile and ran 0.9 % slower on 8192 x 8960 x
+  // 1536.)
+  const int cus = cu_count();
+  if (kPersistent && chunked && ch.family == F16ACC_FAMILY_FAST && p.mode == kWhole && !p.defer_redo && K > 0 &&
+      ch.tile == F16ACC_TILE_256x256 && scn == 1 && ((uintptr_t)c % 4) == 0 && p.tiles_m * p.tiles_n > cus &&
+      cus % kNumXcd == 0) {
+    return ch.blayout == kKC ? (int)launch_persistent<Cfg0<kKC>>(p, out32, cus, st)
+                             : (int)launch_persistent<Cfg0<kNC>>(p, out32, cus, st);
+  }
   int rc = launch(p);
   if (rc == 0 && p.defer_redo) return split_redo(p, redo_ws, ch.blayout, out32, st);
+  if (rc == 0 && p.list) {
+    // the redo launch of the tiles the chunked launch listed: four 128x128
+    // quarters a tile, one workgroup per CU (each takes ceil(quarters / CUs))
+    const int64_t quarters = 4 * p.tiles_m * p.tiles_n;
+    const int grid = (int)(quarters < (int64_t)cus ? quarters : (int64_t)cus);
+    return ch.blayout == kKC ? (int)launch_redo_list<Cfg3<kKC>>(p, out32, grid, st)
+                             : (int)launch_redo_list<Cfg3<kNC>>(p, out32, grid, st);
+  }
   if (rc != 0 || p.mode != kPartial) return rc;
   p.mode = kFinish;
   switch (ch.tile) {  // 256x256 and 64x64 never split (plan_split)
@@ -2137,15 +2447,17 @@ int gemm_impl(const void* a, const void* b, const void* bias, void* c, uint8_t* 
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// Fixed split-K scratch for f16acc_gemm_noalloc: one array per GPU, held
-// from the library's first use on that GPU until the process ends.  A split
-// plan needs at most (workgroup slots) x (tile bytes in FP32): 512 x 64 KiB
-// for 128x128 and 256 x 128 KiB for 256x128 on a 256-CU MI355X, 32 MiB
-// either way.  Every split tile writes all of its partials before the
-// finishing launch reads them, so the array needs no clearing between calls.
-// Calls that overlap in time on one GPU share it and race.
+// Fixed workspace for f16acc_gemm_noalloc: one array per GPU (zero when the
+// code object loads), held until the process ends.  It starts with the
+// deferred redo list (F16ACC_WS_HEADER bytes, which every call leaves zero);
+// the split-K partials follow.  A split plan needs at most (workgroup slots)
+// x (tile bytes in FP32): 512 x 64 KiB for 128x128 and 256 x 128 KiB for
+// 256x128 on a 256-CU MI355X, 32 MiB either way.  Every split tile writes
+// all of its partials before the finishing launch reads them, so they need
+// no clearing between calls.  Calls that overlap in time on one GPU share it
+// and race.
 // ---------------------------------------------------------------------------
-constexpr size_t kScratchBytes = (size_t)32 << 20;
+constexpr size_t kScratchBytes = ((size_t)32 << 20) + F16ACC_WS_HEADER;
 static __device__ __align__(256) char scratch[kScratchBytes];
 
 namespace {
@@ -2177,14 +2489,14 @@ int scratch_ptr(void** out) {
 
 extern "C" {
 
-int f16acc_abi_version(void) { return 6; }
+int f16acc_abi_version(void) { return 7; }
 
 const char* f16acc_strerror(int code) {
   if (code == 0) return "success";
   if (code == F16ACC_E_ARG) return "f16acc: invalid argument";
   if (code == F16ACC_E_UNSUPPORTED) return "f16acc: unsupported layout or extent";
   if (code == F16ACC_E_SCRATCH)
-    return "f16acc: the split-K plan needs more than the 32 MiB fixed scratch of f16acc_gemm_noalloc";
+    return "f16acc: the split-K plan needs more than the fixed scratch of f16acc_gemm_noalloc (32 MiB + header)";
   if (code == F16ACC_E_DEVICE) return "f16acc: the stream belongs to another device than the current one";
   if (code > 0) return hipGetErrorString((hipError_t)code);
   return "f16acc: unknown error";
@@ -2266,7 +2578,8 @@ int f16acc_workspace_size(int64_t M, int64_t N, int64_t K, int64_t sam, int64_t 
   if (M == 0 || N == 0) return 0;
   canon_strides(M, N, K, &sam, &sbk, &sbn);
   const Choice ch = choose(M, N, K, sam, sak, sbk, sbn, a, b, -1);
-  *bytes = plan_split(ch, M, N, K, cu_count()).bytes;
+  const size_t split = plan_split(ch, M, N, K, cu_count()).bytes;
+  *bytes = split > 0 || deferred_redo(ch, M, N, K, cu_count()) ? F16ACC_WS_HEADER + split : 0;
   return 0;
 }
 

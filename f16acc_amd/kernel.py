@@ -25,7 +25,8 @@ PACK_MIN_MACS = 1 << 24
 # f16acc_tile_config's kernel families (F16ACC_FAMILY_* in include/f16acc.h)
 _FAMILIES = ("fast", "generic", "reg")
 
-# Split-K workspace for the FP32 partials, one per (device, stream): kernels
+# Workspace (f16acc_gemm_ws): the deferred redo list of flagged tiles, then
+# the split-K FP32 partials; one per (device, stream): kernels
 # on one stream run one after another, so consecutive calls on a stream can
 # share it.  A workspace that a larger one replaces is kept, not freed: a HIP
 # graph captured earlier holds its address and writes there on every replay,
@@ -97,6 +98,7 @@ def _workspace(a, b, M, N, K):
             _retired.append(ws)
         grown = 2 * ws.numel() if ws is not None else 0
         ws = torch.empty(max(nbytes, grown, 1 << 20), dtype=torch.uint8, device=a.device)
+        ws[:_lib.WS_HEADER].zero_()  # the deferred redo list: empty (the library keeps it so)
         _workspaces[skey] = ws
     return ws
 

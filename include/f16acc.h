@@ -41,6 +41,12 @@ extern "C" {
 #define F16ACC_TILE_256x288 8    /* 8 waves of 64x144; K-contiguous b (else runs as 256x256) */
 #define F16ACC_NUM_TILES 9
 
+/* The first F16ACC_WS_HEADER bytes of a workspace (f16acc_gemm_ws,
+ * f16acc_gemm_tile_ws) hold the list of tiles whose FP32 redo is deferred to
+ * a second launch; they must be zero when the workspace is first used, and
+ * every call leaves them zero.  Split-K partials follow them. */
+#define F16ACC_WS_HEADER 4096
+
 #define F16ACC_FAMILY_FAST 0    /* direct global -> LDS copies of 16-byte units */
 #define F16ACC_FAMILY_GENERIC 1 /* strided element gather through registers */
 #define F16ACC_FAMILY_REG 2     /* unit-stride rows at any even address: 16-byte loads
@@ -99,26 +105,37 @@ int f16acc_gemm_bias(const void* a, const void* b, const void* bias, void* c, ui
                      int out_dtype, int chunked, void* stream);
 
 /*
- * Workspace that lets f16acc_gemm_ws split K for this problem (0 when the
- * problem's tiles already fill the GPU, or its operands take the generic
- * path).  Shapes with few output tiles (k/v projections, 2048 x 256) leave
- * most CUs idle; splitting K into chunk-aligned ranges fills them.
+ * Workspace that f16acc_gemm_ws uses for this problem: F16ACC_WS_HEADER
+ * bytes plus the split-K partials, or 0 when it needs none.  Shapes with
+ * few output tiles (k/v projections, 2048 x 256) leave most CUs idle;
+ * splitting K into chunk-aligned ranges fills them.  Shapes of at most one
+ * round of 256x256 tiles (4096^3) use the header alone: their tiles that
+ * overflow are listed there and redone by a second launch (see
+ * f16acc_gemm_ws).
  */
 int f16acc_workspace_size(int64_t M, int64_t N, int64_t K,
                           int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
                           const void* a, const void* b, size_t* bytes);
 
 /*
- * f16acc_gemm (bias NULL) or f16acc_gemm_bias (bias non-NULL), splitting K
- * when `workspace` (256-byte aligned, ws_bytes >= f16acc_workspace_size)
- * allows it; with a NULL or smaller workspace it does exactly what they do.
- * A split problem runs two launches on `stream`: workgroups sum K ranges of
- * whole chunk pairs (so the chunks are the reference's, f16acc/kernel.py:
- * 44-49) into FP32 partials in the workspace; then one workgroup per tile
- * adds them in split order, flags the tile when the total is not finite and
- * recomputes it over all of K with FP32 accumulation (kernel.py:70-81), and
- * stores it.  The workspace needs no initialisation; calls that overlap in
- * time need separate workspaces.
+ * f16acc_gemm (bias NULL) or f16acc_gemm_bias (bias non-NULL), with a
+ * workspace (256-byte aligned, ws_bytes >= f16acc_workspace_size, its first
+ * F16ACC_WS_HEADER bytes zero on first use); with a NULL or smaller
+ * workspace it does exactly what they do.
+ *   - A split problem runs two launches on `stream`: workgroups sum K ranges
+ *     of whole chunk pairs (so the chunks are the reference's,
+ *     f16acc/kernel.py:44-49) into FP32 partials in the workspace; then one
+ *     workgroup per tile adds them in split order, flags the tile when the
+ *     total is not finite and recomputes it over all of K with FP32
+ *     accumulation (kernel.py:70-81), and stores it.
+ *   - A problem of at most one round of 256x256 tiles runs as f16acc_gemm,
+ *     except that a flagged tile is appended to the header's list instead of
+ *     being redone by its own workgroup, and a second launch always follows:
+ *     each flagged tile is recomputed in FP32 as four 128x128 quarters by
+ *     four workgroups, and the launch's workgroups leave at once when the list
+ *     is empty (the reference's separate _redo launch, kernel.py:75-81,
+ *     103-104).  The last of them empties the list again.
+ * Calls that overlap in time need separate workspaces.
  */
 int f16acc_gemm_ws(const void* a, const void* b, const void* bias, void* c, uint8_t* tile_flags,
                    int64_t M, int64_t N, int64_t K,
@@ -128,9 +145,9 @@ int f16acc_gemm_ws(const void* a, const void* b, const void* bias, void* c, uint
 
 /*
  * f16acc_gemm_ws without a caller workspace and without any allocation: the
- * split-K partials go to a fixed 32 MiB scratch array that the library
- * holds in device memory on each GPU it runs on, from its first use there
- * until the process ends.  No counterpart in the reference; it is for
+ * workspace is a fixed scratch array of 32 MiB plus F16ACC_WS_HEADER bytes
+ * that the library's code object holds in device memory on every GPU where
+ * it is loaded, in every process, until the process ends.  No counterpart in the reference; it is for
  * callers that cannot allocate (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  Same arguments and results as
  * f16acc_gemm_ws (bias may be NULL).
@@ -184,8 +201,8 @@ int f16acc_gemm_tile(const void* a, const void* b, void* c, uint8_t* tile_flags,
  * f16acc_gemm_tile with a split-K workspace, as f16acc_gemm_ws: a forced
  * 256x128, 128x256 or 128x128 tile whose tiles leave CUs idle splits K the
  * way the table's own 128x128 pick does (the 256x256 and 64x64 tiles never
- * split).  A workspace of 32 MiB covers every split on a 256-CU GPU; a
- * smaller one runs the problem unsplit.  For tuning, and for testing the
+ * split).  A workspace of 32 MiB + F16ACC_WS_HEADER covers every split on a
+ * 256-CU GPU; a smaller one runs the problem unsplit.  For tuning, and for testing the
  * split path on every tile that has one.
  */
 int f16acc_gemm_tile_ws(const void* a, const void* b, void* c, uint8_t* tile_flags,

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(dll, name), name
     assert sorted(_lib.EXPORTS) == names
-    assert _lib.abi_version() == _lib.ABI_VERSION == 6
+    assert _lib.abi_version() == _lib.ABI_VERSION == 7
 
 
 def test_gemm_rejects_bad_arguments_before_launching():
@@ -350,3 +350,18 @@ def test_k_split_only_where_cus_would_idle():
         sbk, sbn = (1, K) if b_kc else (N, 1)
         _lib.check(_lib.workspace_size(M, N, K, K, 1, sbk, sbn, 0, 0, ctypes.byref(n)))
         assert (n.value > 0) == split, (M, N, K, b_kc)
+
+
+def test_workspace_holds_the_redo_list_where_it_is_deferred():
+    """f16acc_workspace_size: one round of 256x256 tiles (4096^3) needs the
+    header alone (its flagged tiles are listed and redone by a second launch);
+    more rounds (8192^3: the persistent kernel redoes in place) and shapes
+    whose tiles fill the CUs on other tiles need nothing; a split-K plan needs
+    the header plus its partials."""
+    n = ctypes.c_size_t()
+    for (M, N, K, sbk, sbn), want in (((4096, 4096, 4096, 4096, 1), "header"), ((4096, 4096, 4096, 1, 4096), "header"),
+                                      ((8192, 8192, 8192, 8192, 1), "none"), ((2048, 2048, 1536, 1, 1536), "none"),
+                                      ((2048, 1536, 8960, 1536, 1), "split")):
+        _lib.check(_lib.workspace_size(M, N, K, K, 1, sbk, sbn, 0, 0, ctypes.byref(n)))
+        got = "none" if n.value == 0 else "header" if n.value == _lib.WS_HEADER else "split"
+        assert got == want, (M, N, K, n.value)

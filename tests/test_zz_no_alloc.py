@@ -1,9 +1,11 @@
-"""f16acc_gemm_noalloc, the entry point that allocates nothing: split-K
-partials go to the library's fixed per-GPU scratch instead of a caller
-workspace.  Called through the C ABI, it returns the same bits and tile flags
-as f16acc_gemm_ws with a caller workspace, on two calls in a row (the second
-smaller), both split along K, and the GPU's free memory does not change
-across a call."""
+"""f16acc_gemm_noalloc, the entry point that allocates nothing: the
+workspace (deferred redo list, split-K partials) is the library's fixed
+per-GPU scratch instead of a caller's.  Called through the C ABI, it returns
+the same bits and tile flags as f16acc_gemm_ws with a caller workspace, on
+two calls in a row (the second smaller), both split along K, and the GPU's
+free memory does not change across a call; on a shape whose flagged tiles
+are redone by the deferred list, it equals f16acc_gemm (redo in place) on
+consecutive calls, so the scratch's list is left empty."""
 
 import pytest
 import torch
@@ -38,7 +40,7 @@ def _split_bytes(a, b):
     n = ctypes.c_size_t()
     _lib.check(_lib.workspace_size(M, b.shape[1], K, a.stride(0), a.stride(1), b.stride(0), b.stride(1),
                                    a.data_ptr(), b.data_ptr(), ctypes.byref(n)))
-    return n.value
+    return max(n.value - _lib.WS_HEADER, 0)  # the split-K partials' bytes
 
 
 def _overflow_case():
@@ -57,7 +59,8 @@ def _overflow_case():
 def test_noalloc_equals_workspace_entry_on_two_calls_in_a_row():
     from f16acc_amd.kernel import tile_config
 
-    ws = torch.empty(32 << 20, dtype=torch.uint8, device="cuda")
+    ws = torch.empty((32 << 20) + _lib.WS_HEADER, dtype=torch.uint8, device="cuda")
+    ws[:_lib.WS_HEADER].zero_()
     # call 1: the Qwen2.5-1.5B down projection's shape (2048 x 1536 x 8960,
     # fused bias, fp16 out) with the weight row-major [K, N] (b = w.t() would
     # split K inside the workgroup instead), split in two on 128x128 tiles
@@ -101,14 +104,22 @@ def test_noalloc_equals_workspace_entry_on_two_calls_in_a_row():
 
 
 def test_noalloc_unsplit_problem_equals_plain_entry():
-    """A problem whose tiles fill the GPU takes no split: the same bits as
-    f16acc_gemm (4096 x 4096 x 1024, fp16 out)."""
-    a, b = rnd((4096, 1024), 85).cuda(), rnd((1024, 4096), 86).cuda()
+    """A problem whose tiles fill the GPU takes no split (4096 x 4096 x 1024,
+    one round of 256x256 tiles, fp16 out); its overflowing tiles are listed in
+    the scratch's header and redone by a second launch.  Three calls in a row
+    (overflow, clean, overflow) each equal f16acc_gemm, which redoes in place,
+    bit for bit: the list is emptied after each call."""
+    a, b = rnd((4096, 1024), 85), rnd((1024, 4096), 86)
+    a[512:640] = 120.0  # 128 rows x 128 columns whose chunk sums pass 65504
+    b[:, 1024:1152] = 120.0
+    clean_a = rnd((4096, 1024), 87).cuda()
+    a, b = a.cuda(), b.cuda()
     assert _split_bytes(a, b) == 0
-    c = torch.empty(4096, 4096, device="cuda", dtype=torch.float16)
-    _call(_lib.gemm_noalloc, a, b, None, c, None)
-    plain = torch.empty_like(c)
-    _lib.check(_lib.gemm(a.data_ptr(), b.data_ptr(), plain.data_ptr(), None, 4096, 4096, 1024, 1024, 1, 4096, 1,
-                         4096, 1, _lib.OUT_F16, 1, torch.cuda.current_stream().cuda_stream))
-    torch.cuda.synchronize()
-    assert torch.equal(c, plain)
+    for x in (a, clean_a, a):
+        c = torch.empty(4096, 4096, device="cuda", dtype=torch.float16)
+        _call(_lib.gemm_noalloc, x, b, None, c, None)
+        plain = torch.empty_like(c)
+        _lib.check(_lib.gemm(x.data_ptr(), b.data_ptr(), plain.data_ptr(), None, 4096, 4096, 1024, 1024, 1, 4096, 1,
+                             4096, 1, _lib.OUT_F16, 1, torch.cuda.current_stream().cuda_stream))
+        torch.cuda.synchronize()
+        assert torch.equal(c, plain)
