@@ -106,23 +106,24 @@ static_assert(kStageK == 2 * kChunk, "a stage holds exactly one chunk pair");
 // workspace (zero when first used; left zero by every call): the chunked
 // launch appends each flagged tile's id, the redo launch that follows
 // recomputes those tiles, and its last workgroup empties the list again.
-// The redo launch's workgroups count themselves done on kDoneLines counters,
-// each on its own 128-byte line (device-scope atomics on one address
-// serialise: one counter for 512 workgroups cost ~9 us a call), and the last
-// workgroup of each counter on one more.
-constexpr int kDoneLines = 8;
+// The list is read through kLines copies of its length, each on its own
+// 128-byte line beside a count of the redo launch's workgroups that have read
+// it (one 64-bit word: done << 32 | length): workgroup b takes line b %
+// kLines, and one atomic add of 1 << 32 both reads the length and counts the
+// workgroup; the line's last workgroup clears it.  (Device-scope atomics on
+// one address serialise: one counter for 512 workgroups cost ~9 us a call,
+// and three dependent round trips per workgroup ~4 us.)
+constexpr int kLines = 8;
 struct RedoList {
-  int count;  // tiles appended (an atomic counter)
+  int alloc;  // the chunked launch's next free item (an atomic counter)
   int pad0[31];
-  int groups_done;  // counters whose workgroups have all finished
-  int pad1[31];
   struct {
-    int n;
-    int pad[31];
-  } done[kDoneLines];  // finished workgroups with blockIdx.x % kDoneLines == j
-  int items[(F16ACC_WS_HEADER - 128 * (2 + kDoneLines)) / 4];
+    unsigned long long word;  // done << 32 | number of items listed
+    int pad[30];
+  } line[kLines];
+  int items[(F16ACC_WS_HEADER - 128 * (1 + kLines)) / 4];
 };
-constexpr int kRedoMax = (F16ACC_WS_HEADER - 128 * (2 + kDoneLines)) / 4;
+constexpr int kRedoMax = (F16ACC_WS_HEADER - 128 * (1 + kLines)) / 4;
 static_assert(sizeof(RedoList) == F16ACC_WS_HEADER, "the list fills the workspace header");
 
 __device__ __forceinline__ int load_agent(const int* p) {
@@ -918,7 +919,11 @@ __device__ __forceinline__ void k_loop_cross(const Params& p, int64_t m0, int64_
   __syncthreads();  // LDS free for the store's staging
 }
 
-template <class C, bool CHUNKED>
+// ONE_PHASE: every K group runs the early groups' loop on a two-stage ring
+// (a late group's three-stage area holds it), for the rare FP32 redo of a
+// chunked kernel: one K-loop instantiation instead of two keeps that kernel's
+// code, and its instruction-cache misses, smaller.
+template <class C, bool CHUNKED, bool ONE_PHASE = false>
 __device__ __forceinline__ void k_groups_fast(const Params& p, int64_t m0, int64_t n0, int64_t kbeg, int64_t kend,
                                               char LDS_AS* smem, FastLoader<C>& ld, int g, int ltid, int lw, int wm,
                                               int wn, int lane, f32x4 (&acc)[C::FM][C::FN],
@@ -929,7 +934,7 @@ __device__ __forceinline__ void k_groups_fast(const Params& p, int64_t m0, int64
   }
   int64_t gbeg = kbeg, gend = kend, iters = 0;
   if (C::KG > 1) iters = group_range<C>(kbeg, kend, g, &gbeg, &gend);
-  if (C::SPLIT && g >= C::KG / 2)  // wave-uniform
+  if (C::SPLIT && !ONE_PHASE && g >= C::KG / 2)  // wave-uniform
     k_loop_fast<C, CHUNKED, true>(p, m0, n0, gbeg, gend, smem + C::ring_base(g), ld, lw, wm, wn, lane, acc, iters);
   else
     k_loop_fast<C, CHUNKED>(p, m0, n0, gbeg, gend, smem + C::ring_base(g), ld, lw, wm, wn, lane, acc, iters);
@@ -1408,7 +1413,7 @@ __device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, 
       for (int i = 0; i < C::FM; ++i)
 #pragma unroll
         for (int j = 0; j < C::FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      k_groups_fast<C, false>(p, m0, n0, 0, p.K, smem, ld, g, ltid, lw, wm, wn, lane, acc);
+      k_groups_fast<C, false, true>(p, m0, n0, 0, p.K, smem, ld, g, ltid, lw, wm, wn, lane, acc);
     }
   } else if constexpr (CHUNKED && kRedo) {
     // tile flag: any element of the FP32 sum inf or NaN (kernel.py:70-71)
@@ -1433,9 +1438,13 @@ __device__ __forceinline__ void finish_tile(const Params& p, char LDS_AS* smem, 
       // carries the outcome once every wave has read the flag.
       __syncthreads();
       if (tid == 0) {
-        const int idx = atomicAdd(&p.list->count, 1);
+        const int idx = atomicAdd(&p.list->alloc, 1);
         const bool listed = idx >= 0 && idx < kRedoMax;
-        if (listed) store_agent(&p.list->items[idx], (int)(tm * p.tiles_n + tn));
+        if (listed) {
+          store_agent(&p.list->items[idx], (int)(tm * p.tiles_n + tn));
+#pragma unroll
+          for (int j = 0; j < kLines; ++j) atomicAdd(&p.list->line[j].word, 1ull);
+        }
         *tf.word = listed ? 2 : 1;
       }
       __syncthreads();
@@ -1579,9 +1588,8 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) 
 // (128x128, the chunked launch's b layout), over all of K in order: each
 // element sums exactly what the in-place redo sums, in the same order (same
 // bits).  p.tiles_n is the 256x256 grid's.  Every workgroup leaves at once
-// when the list is empty; the last to finish empties it for the next call
-// (all have read the count by then: each reads it before counting itself
-// done, on the RedoList counters).
+// when the list is empty, and the list is empty again once every workgroup
+// has read its length (RedoList).
 template <class C, bool OUT32>
 __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) void redo_list_kernel(Params p) {
   static_assert(C::BM == 128 && C::BN == 128 && C::KG == 1, "quarters of 256x256 tiles");
@@ -1591,7 +1599,23 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
-  int count = __builtin_amdgcn_readfirstlane(load_agent(&p.list->count));
+  __shared__ int listed;
+  if (tid == 0) {
+    // read this line's copy of the list length and count this workgroup in
+    // one atomic; the line's last workgroup clears it (every other one has
+    // read it by then), and workgroup 0 clears the chunked launch's counter
+    const int G = (int)gridDim.x, j = (int)(blockIdx.x % kLines);
+    const int members = (G - j + kLines - 1) / kLines;
+    const unsigned long long old = atomicAdd(&p.list->line[j].word, 1ull << 32);
+    if ((int)(old >> 32) == members - 1) atomicExch(&p.list->line[j].word, 0ull);
+    if (blockIdx.x == 0) {
+      atomicExch(&p.list->alloc, 0);
+      for (int l = G; l < kLines; ++l) atomicExch(&p.list->line[l].word, 0ull);  // lines no workgroup reads
+    }
+    listed = (int)(uint32_t)old;
+  }
+  __syncthreads();
+  int count = __builtin_amdgcn_readfirstlane(listed);
   count = count < 0 ? 0 : count > kRedoMax ? kRedoMax : count;
   const int64_t tiles = p.tiles_m * p.tiles_n;
   for (int64_t item = blockIdx.x; item < 4 * (int64_t)count; item += gridDim.x) {
@@ -1610,17 +1634,6 @@ __global__ __launch_bounds__(C::T) __attribute__((amdgpu_waves_per_eu(C::WPE))) 
     k_loop_fast<C, false>(p, m0, n0, 0, p.K, smem, ld, wave, wm, wn, lane, acc);
     store_any<C, OUT32, kSmem>(p, smem, m0, n0, wave, wm, wn, lane, acc);
     __syncthreads();  // staging reads done before the next quarter's copies
-  }
-  if (tid == 0) {
-    const int G = (int)gridDim.x, j = (int)(blockIdx.x % kDoneLines);
-    const int members = (G - j + kDoneLines - 1) / kDoneLines, lines = G < kDoneLines ? G : kDoneLines;
-    if (atomicAdd(&p.list->done[j].n, 1) == members - 1) {
-      store_agent(&p.list->done[j].n, 0);
-      if (atomicAdd(&p.list->groups_done, 1) == lines - 1) {
-        store_agent(&p.list->count, 0);
-        store_agent(&p.list->groups_done, 0);
-      }
-    }
   }
 }
 

@@ -31,10 +31,11 @@ def _ws():
 
 
 def _counters_zero(ws):
-    """The list's counters (count, counters finished, 8 done counters: the
-    first int of each 128-byte line of the header's first 1280 bytes) are
-    back to zero."""
-    return int(ws[:1280].view(torch.int32)[::32].abs().sum()) == 0
+    """The list's counters (the chunked launch's item counter and the 8 lines
+    of length and readers: the first 8 bytes of each 128-byte line of the
+    header's first 1152 bytes) are back to zero."""
+    lines = ws[:1152].view(torch.int32).view(9, 32)[:, :2]
+    return int(lines.abs().sum()) == 0
 
 
 def _gemm(a, b, c, bias=None, flags=None, ws=None):
@@ -110,6 +111,31 @@ def test_deferred_redo_equals_redo_in_place(M, N, K, rows, cols, b_t, out_dtype,
     fin = torch.isfinite(ref)
     err = (outs[0].cpu()[fin].double() - ref[fin].double()).abs().max() / ref[fin].double().abs().max()
     assert float(err) < 1e-3
+
+
+def test_one_tile_grid_between_full_grids_on_one_workspace():
+    """256x256 forced (f16acc_gemm_tile_ws against f16acc_gemm_tile, which
+    redoes in place): a 4096^3-row call, then a one-tile problem (a redo
+    launch of 4 workgroups, fewer than the list's 8 lines: the lines no
+    workgroup reads are cleared too), then the first call again; every call
+    equals the in-place redo, so no line keeps a stale length."""
+    ws = _ws()
+    tile = _lib.TILES.index("256x256")
+    big = _overflowing(4096, 4096, 512, [3, 17], [6, 25], 9)
+    small = _overflowing(256, 256, 256, [0], [1], 10)
+    for a, b in (big, small, big):
+        ga, gb = a.cuda(), b.cuda()
+        M, K = a.shape
+        N = b.shape[1]
+        c0 = torch.empty(M, N, device="cuda", dtype=torch.float32)
+        c1 = torch.empty_like(c0)
+        args = (M, N, K, K, 1, N, 1, N, 1, _lib.OUT_F32, 1, torch.cuda.current_stream().cuda_stream, tile)
+        _lib.check(_lib.gemm_tile(ga.data_ptr(), gb.data_ptr(), c0.data_ptr(), None, *args))
+        _lib.check(_lib.gemm_tile_ws(ga.data_ptr(), gb.data_ptr(), c1.data_ptr(), None, *args, ws.data_ptr(),
+                                     ws.numel()))
+        torch.cuda.synchronize()
+        assert torch.equal(c0, c1), M
+        assert _counters_zero(ws)
 
 
 def test_every_tile_flagged_and_none_flagged():
