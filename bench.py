@@ -7,13 +7,16 @@ timed op first runs back to back for 0.2 s so the GPU clock has settled, then
 W warm-up steps, then exactly K timed steps.  The
 default workload is the headline one: M = N = K = 4096, A and B ~ N(0, 1)
 cast to fp16, B row-major [K, N] (as the reference's bench/gemm_bench.py
-passes it), fp16 output, chunk-32 with FP32 chunk sum and in-kernel overflow
-redo.  Prints one JSON line:
+passes it), fp16 output, chunk-32 with FP32 chunk sum and FP32 redo of
+overflowing tiles (at this shape by a second launch that leaves at once when
+no tile overflowed).  Prints one JSON line:
   value       TFLOPS of the timed steps (2 M N K per step)
-  roofline    the GEMM kernel's achieved TFLOP/s (HIP events over the timed
-              region on the launch stream) against the MI355X dense fp16
-              MFMA peak; traffic = HBM bytes per launch from the rocprofv3
-              FETCH_SIZE / WRITE_SIZE summary in profiles/, when present
+  roofline    the GEMM kernel's achieved TFLOP/s (the kernel launched alone
+              through f16acc_gemm, HIP events over its timed region on the
+              launch stream) against the MI355X dense fp16 MFMA peak;
+              traffic = HBM bytes per launch from the rocprofv3 FETCH_SIZE /
+              WRITE_SIZE summary in profiles/, when present; call_us = per
+              mm call, both launches
   cpu_baseline the reference algorithm (the CPU oracle) on this host's cores
   hipblaslt   torch.mm (hipBLASLt) on the same inputs and GPU
   max_rel_err_vs_fp64 / max_rel_err_vs_oracle  the reference's error metric
@@ -447,16 +450,20 @@ def overflow_bench(steps, warmup):
 
 
 def overflow_split_redo(rounds=5):
-    """The overflow stress workload on the shipped library (each flagged
-    tile redone in FP32 by its own workgroup, a straggler on its CU) against
-    libf16acc_amd_splitredo.so (-DF16ACC_SPLIT_REDO=1: the chunked launch
-    only flags; flagged tiles are recomputed in FP32 as 128x128 tiles split
-    three ways along K, plus a finishing launch; loaded here only), both on
-    the stress data and on its no-overflow twin, through f16acc_gemm with
-    the same inputs, timed in interleaved settled bursts (median over
-    rounds).  Checks: the same flags; unflagged tiles bit-equal; flagged
-    tiles against the FP32-accumulate mode (a different FP32 summation
-    order: the three K ranges are summed after)."""
+    """The overflow stress workload through three redo schemes, on the stress
+    data and on its no-overflow twin, with the same inputs, timed in
+    interleaved settled bursts (median over rounds):
+      in_place  f16acc_gemm (no workspace): each flagged tile redone in FP32 by
+                its own workgroup, a straggler on its CU;
+      deferred  f16acc_gemm_ws (the entry mm uses): flagged tiles listed in the
+                workspace header and redone by a second launch as 128x128
+                quarters, one workgroup each;
+      split     libf16acc_amd_splitredo.so (-DF16ACC_SPLIT_REDO=1, loaded
+                here only): the chunked launch only flags; flagged tiles are
+                recomputed as 128x128 tiles split three ways along K, plus a
+                finishing launch.
+    Checks: the same flags; unflagged tiles bit-equal; redone tiles against
+    the FP32-accumulate mode (the split sums its three K ranges after)."""
     import ctypes
 
     from f16acc_amd import _lib, build
@@ -470,19 +477,26 @@ def overflow_split_redo(rounds=5):
     _, _, ca, cb = make_inputs(a_cpu.shape[0], b_cpu.shape[1], a_cpu.shape[1], "row")
     data["clean"] = (ca, cb)
     st = torch.cuda.current_stream().cuda_stream
+    ws = torch.empty(_lib.WS_HEADER, dtype=torch.uint8, device="cuda")
+    ws.zero_()
     out = {}
     times = {}
     for dname, (a, b) in data.items():
         M, K = a.shape
         N = b.shape[1]
         cfg = tile_config(a, b)
-        for lname, fn in (("shipped", _lib.gemm), ("split_redo", g_split)):
+        for lname, fn in (("in_place", _lib.gemm), ("deferred", None), ("split", g_split)):
             c = torch.empty(M, N, device="cuda", dtype=torch.float32)
             fl = torch.zeros(cfg["tiles_m"] * cfg["tiles_n"], device="cuda", dtype=torch.uint8)
 
             def call(c=c, fl=None, fn=fn, a=a, b=b):
-                _lib.check(fn(a.data_ptr(), b.data_ptr(), c.data_ptr(), fl, M, N, K, a.stride(0), a.stride(1),
-                              b.stride(0), b.stride(1), c.stride(0), c.stride(1), _lib.OUT_F32, 1, st))
+                args = (M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1), c.stride(0), c.stride(1),
+                        _lib.OUT_F32, 1, st)
+                if fn is None:
+                    _lib.check(_lib.gemm_ws(a.data_ptr(), b.data_ptr(), None, c.data_ptr(), fl, *args, ws.data_ptr(),
+                                            ws.numel()))
+                else:
+                    _lib.check(fn(a.data_ptr(), b.data_ptr(), c.data_ptr(), fl, *args))
 
             call(fl=fl.data_ptr())
             torch.cuda.synchronize()
@@ -493,23 +507,29 @@ def overflow_split_redo(rounds=5):
             ts.append(settled_time(call))
     a, b = data["overflow"]
     cfg = tile_config(a, b)
-    (c_ship, f_ship), (c_split, f_split) = out[("overflow", "shipped")], out[("overflow", "split_redo")]
+    c_in, f_in = out[("overflow", "in_place")]
     c32 = mm_tile(a, b, cfg["tile"], torch.float32, chunked=False)
     bm, bn = cfg["bm"], cfg["bn"]
-    M, N = c_ship.shape
-    mask = f_ship.view(cfg["tiles_m"], cfg["tiles_n"]).bool().repeat_interleave(bm, 0).repeat_interleave(bn, 1)[:M, :N]
+    M, N = c_in.shape
+    mask = f_in.view(cfg["tiles_m"], cfg["tiles_n"]).bool().repeat_interleave(bm, 0).repeat_interleave(bn, 1)[:M, :N]
     ref = c32[mask].double()
     us = {f"{d}_{l}_us": round(statistics.median(ts) * 1e6, 2) for (d, l), (_, ts) in times.items()}
-    line = {"workload": "overflow stress 4096^3, fp32 out, B row-major: in-kernel redo vs split redo",
-            "tile": cfg["tile"], "flagged_tiles": int(f_ship.sum()), "same_flags": bool(torch.equal(f_ship, f_split)),
-            **us,
-            "overflow_cost_shipped_pct": round((us["overflow_shipped_us"] / us["clean_shipped_us"] - 1) * 100, 1),
-            "overflow_cost_split_pct": round((us["overflow_split_redo_us"] / us["clean_shipped_us"] - 1) * 100, 1),
-            "split_redo_clean_cost_pct": round((us["clean_split_redo_us"] / us["clean_shipped_us"] - 1) * 100, 1),
-            "unflagged_bit_equal": bool(torch.equal(c_ship[~mask], c_split[~mask])),
-            "shipped_redone_equal_fp32_mode": bool(torch.equal(c_ship[mask], c32[mask])),
-            "split_redone_max_rel_diff_vs_fp32_mode": ((c_split[mask].double() - ref).abs().max() / ref.abs().max()).item(),
-            "clean_outputs_bit_equal": bool(torch.equal(out[("clean", "shipped")][0], out[("clean", "split_redo")][0]))}
+    clean = us["clean_in_place_us"]
+    line = {"workload": "overflow stress 4096^3, fp32 out, B row-major: redo in place vs deferred list vs split",
+            "tile": cfg["tile"], "flagged_tiles": int(f_in.sum()),
+            "same_flags": all(torch.equal(out[("overflow", k)][1], f_in) for k in ("deferred", "split")), **us,
+            **{f"overflow_cost_{k}_pct": round((us[f"overflow_{k}_us"] / clean - 1) * 100, 1)
+               for k in ("in_place", "deferred", "split")},
+            **{f"clean_cost_{k}_pct": round((us[f"clean_{k}_us"] / clean - 1) * 100, 1) for k in ("deferred", "split")},
+            "unflagged_bit_equal": all(torch.equal(out[("overflow", k)][0][~mask], c_in[~mask])
+                                       for k in ("deferred", "split")),
+            "in_place_and_deferred_redone_equal_fp32_mode": bool(torch.equal(c_in[mask], c32[mask]) and
+                                                                 torch.equal(out[("overflow", "deferred")][0][mask],
+                                                                             c32[mask])),
+            "split_redone_max_rel_diff_vs_fp32_mode": ((out[("overflow", "split")][0][mask].double() - ref).abs().max()
+                                                       / ref.abs().max()).item(),
+            "clean_outputs_bit_equal": all(torch.equal(out[("clean", k)][0], out[("clean", "in_place")][0])
+                                           for k in ("deferred", "split"))}
     print(json.dumps(line), flush=True)
 
 
@@ -692,6 +712,29 @@ def copy_reference(steps, warmup, nbytes=1 << 30):
                       "GB_per_s": round(2 * nbytes * steps / ev / 1e9, 1), "steps": steps}), flush=True)
 
 
+def _gemm_kernel_op(a, b, out_dtype):
+    """One f16acc_gemm launch on HBM-resident a, b into a preallocated c, for
+    a problem whose mm call is that launch plus the deferred redo launch (its
+    workspace is the redo list alone); None for any other problem."""
+    import ctypes
+
+    from f16acc_amd import _lib
+
+    M, K = a.shape
+    N = b.shape[1]
+    n = ctypes.c_size_t()
+    _lib.check(_lib.workspace_size(M, N, K, a.stride(0), a.stride(1), b.stride(0), b.stride(1), a.data_ptr(),
+                                   b.data_ptr(), ctypes.byref(n)))
+    if n.value != _lib.WS_HEADER:
+        return None
+    c = torch.empty(M, N, device=a.device, dtype=out_dtype)
+    code = _lib.OUT_F32 if out_dtype == torch.float32 else _lib.OUT_F16
+    stream = torch.cuda.current_stream().cuda_stream
+    args = (a.data_ptr(), b.data_ptr(), c.data_ptr(), None, M, N, K, a.stride(0), a.stride(1), b.stride(0),
+            b.stride(1), c.stride(0), c.stride(1), code, 1, stream)
+    return lambda: _lib.check(_lib.gemm(*args))
+
+
 def main():
     global PREHEAT_S
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
@@ -754,7 +797,12 @@ def main():
     op = lambda: f16acc_amd.mm(a, b, out_dtype)  # noqa: E731
     wall, ev = time_steps(op, args.steps, args.warmup)
     value = flops * args.steps / wall / 1e12
-    kernel_s = ev / args.steps  # average per launch, HIP events on the launch stream
+    call_s = ev / args.steps  # per mm call (the GEMM kernel, and the redo launch where mm defers it)
+    # The dominant kernel alone: where mm follows the GEMM with the deferred
+    # redo launch, f16acc_gemm (no workspace) launches exactly that GEMM
+    # kernel, once per call; elsewhere the mm call is its kernels.
+    kernel_op = _gemm_kernel_op(a, b, out_dtype) or op
+    kernel_s = time_steps(kernel_op, args.steps, args.warmup)[1] / args.steps
     achieved = flops / kernel_s / 1e12
 
     c = op()
@@ -779,14 +827,16 @@ def main():
         "config": {"workload": f"fp16 GEMM M={M} N={N} K={K}, A,B~N(0,1) seeded, B "
                                f"{'row-major [K,N]' if layout == 'row' else 'w.t() of [N,K]'}, "
                                f"{'fp16' if out_dtype == torch.float16 else 'fp32'} out, chunk-32 + FP32 sum "
-                               f"+ in-kernel overflow redo", "name": args.workload,
+                               f"+ FP32 redo of overflowing tiles", "name": args.workload,
                    "tile": f"{cfg['bm']}x{cfg['bn']}", "tiles": cfg["tiles_m"] * cfg["tiles_n"],
                    "kernel_family": cfg["family"]},
         "frac_of_peak": round(value / PEAK_TFLOPS, 4),
         "max_rel_err_vs_fp64": err_fp64,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": read_traffic(args.workload),
-                     "kernel_us": round(kernel_s * 1e6, 2)},
+                     "kernel_us": round(kernel_s * 1e6, 2), "call_us": round(call_s * 1e6, 2),
+                     "kernel": "the GEMM kernel alone (f16acc_gemm, one launch) where mm adds the deferred redo "
+                               "launch, else the mm call; call_us: per mm call"},
         "hipblaslt": {"value": round(flops / blas_t / 1e12, 2), "unit": "TFLOPS",
                       "op": "torch.mm (hipBLASLt), same inputs", "us": round(blas_t * 1e6, 2)},
         "fp32_accumulate": {"value": round(flops / fp32acc_t / 1e12, 2), "unit": "TFLOPS",
