@@ -19,6 +19,10 @@
 //           then four VALU ops of one class (16 cycles if fully hidden)
 //   part 2  complete chunk epilogues, software pipelined (the epilogue of
 //           block j-2 runs next to the MFMAs of block j)
+//   part 3  the smaller f16 MFMAs (16x16x16, 4x4x4 in 16 blocks): cycles per
+//           instruction, and epilogues that add a chunk pair with two of
+//           them as lane-local identity sums instead of one 16x16x32
+//           selector (the self-check covers those sums too)
 //
 //   usage: chunkrate            (needs one gfx950 GPU; prints a table)
 
@@ -36,6 +40,8 @@ typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x8 __attribute__((ext_vector_type(8)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 #define CHECK(x)                                                                   \
   do {                                                                             \
@@ -108,6 +114,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 #define DOT2(s, h) asm volatile("v_dot2c_f32_f16 %0, %1, %2" : "+v"(s) : "v"(h), "v"(ones))
 #define SMFMAC(acc, a, b, idx) \
   asm volatile("v_smfmac_f32_16x16x64_f16 %0, %1, %2, %3" : "+v"(acc) : "v"(a), "v"(b), "v"(idx))
+#define M16X16X16(acc, a, b) asm volatile("v_mfma_f32_16x16x16_f16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b))
+#define M4X4X4(acc, a, b) asm volatile("v_mfma_f32_4x4x4_16b_f16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b))
+
+// Identity A operands of the lane-local sums (part 3).  v_mfma_f32_16x16x16_f16:
+// lane 16q+n holds A[n][4q+e], B[4q+e][n] and D[4q+r][n]; with A[i][k] = (i == k)
+// each lane adds its own four B halves to its own four D registers.
+// v_mfma_f32_4x4x4_16b_f16 (block l/4): lane l holds A[l%4][e], B[e][l%4] and
+// D[r][l%4]; A[i][k] = (i == k) does the same.
+__device__ __forceinline__ f16x4 identity_16x16x16(int lane) {
+  f16x4 a;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) a[e] = ((lane & 15) == 4 * (lane >> 4) + e) ? (f16)1.0f : (f16)0.0f;
+  return a;
+}
+__device__ __forceinline__ f16x4 identity_4x4x4(int lane) {
+  f16x4 a;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) a[e] = ((lane & 3) == e) ? (f16)1.0f : (f16)0.0f;
+  return a;
+}
 
 // Sparse selector of a chunk quad: with B = {X_odd, X_even} (the rounded
 // pairs of one 16x16 block from two consecutive stages, dense 16x16x32 B
@@ -131,7 +157,10 @@ __device__ __forceinline__ void quad_selector(int lane, f16x8& a, int& idx) {
 //    5 cvt_pk + sparse selector (one v_smfmac_f32_16x16x64_f16 per block per
 //      two stages; the two stages' rounded pairs joined into one 8-register
 //      operand), 6 as 5 with the rounding written straight into that operand
-//    (5 and 6 run an even and an odd stage per iteration: 2 NB steps)
+//    (5 and 6 run an even and an odd stage per iteration: 2 NB steps),
+//    7 cvt_pk x4 (each chunk's four values into two dwords) + two
+//      v_mfma_f32_16x16x16_f16 identity sums, 8 the same with two
+//      v_mfma_f32_4x4x4_16b_f16
 template <int E>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void epilogue_kernel(
     float* out, int iters, unsigned long long* cyc) {
@@ -159,6 +188,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   f16x8 sel4;
   int idx;
   quad_selector(lane, sel4, idx);
+  const f16x4 id = E == 7 ? identity_16x16x16(lane) : identity_4x4x4(lane);
   u32x4 hs[NB];
   u32x8 X[NB];
 #pragma unroll
@@ -216,6 +246,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       if (E == 3) {
         CVT_PK(h[q][0], p0[q][0], p1[q][0]);
         CVT_PK(h[q][1], p0[q][1], p1[q][1]);
+      } else if (E == 7 || E == 8) {
+        CVT_PK(h[q][0], p0[q][0], p0[q][1]);
+        CVT_PK(h[q][1], p0[q][2], p0[q][3]);
       } else {
         CVT_PK(h[q][0], p0[q][0], p1[q][0]);
         CVT_PK(h[q][1], p0[q][1], p1[q][1]);
@@ -233,6 +266,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         CVT_PK(h[q][3], p0[q][3], p1[q][3]);
         const int r = (j + NB - 3) % NB;  // rounded during the previous step
         MFMA_ACC(S[r], sel, h[r]);
+      } else if (E == 7 || E == 8) {
+        CVT_PK(h[q][2], p1[q][0], p1[q][1]);
+        CVT_PK(h[q][3], p1[q][2], p1[q][3]);
+        const int r = (j + NB - 3) % NB;
+        const u32x2 x0 = {h[r][0], h[r][1]}, x1 = {h[r][2], h[r][3]};
+        if (E == 7) {
+          M16X16X16(S[r], id, x0);
+          M16X16X16(S[r], id, x1);
+        } else {
+          M4X4X4(S[r], id, x0);
+          M4X4X4(S[r], id, x1);
+        }
       }
     }
   }
@@ -240,6 +285,45 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   float s = 0.f;
 #pragma unroll
   for (int j = 0; j < NB; ++j) s += S[j][0] + S[j][3] + p0[j][1] + p1[j][2] + (float)h[j][1] + (float)hs[j][2] + (float)X[j][5];
+  out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+  if (threadIdx.x == 0) cyc[blockIdx.x] = t1 - t0;
+}
+
+// ---- part 3: cycles per MFMA of each f16 shape ------------------------------
+// OP 0: v_mfma_f32_16x16x32_f16, 1: v_mfma_f32_16x16x16_f16,
+// 2: v_mfma_f32_4x4x4_16b_f16; 16 independent accumulators back to back.
+template <int OP>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void mfma_rate_kernel(
+    float* out, int iters, unsigned long long* cyc) {
+  const int lane = threadIdx.x & 63;
+  f16x8 a8, b8;
+  f16x4 a4, b4;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    a8[e] = (f16)(0.01f * (lane + e));
+    b8[e] = (f16)(0.02f * (lane - e));
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    a4[e] = a8[e];
+    b4[e] = b8[e];
+  }
+  f32x4 acc[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, (float)j};
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if (OP == 0) MFMA_ACC(acc[j], a8, b8);
+      if (OP == 1) M16X16X16(acc[j], a4, b4);
+      if (OP == 2) M4X4X4(acc[j], a4, b4);
+    }
+  }
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) s += acc[j][0] + acc[j][3];
   out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
   if (threadIdx.x == 0) cyc[blockIdx.x] = t1 - t0;
 }
@@ -256,9 +340,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 // leave
 //   s_in[r] + f16(P0[r]) + f16(P1[r])      (pair)
 //   s_in[r] + f16(P0[r]) + ... + f16(P3[r]) (quad)
-// in that same register.
+// in that same register; and the lane-local identity sums of part 3, one
+// MFMA per chunk (16x16x16 and 4x4x4 forms), must leave
+//   (s_in[r] + f16(P0[r])) + f16(P1[r])     (two FP32 additions in order)
 __global__ __launch_bounds__(64) void selfcheck_kernel(const f16x8* in_a, const f16x8* in_b, const f32x4* s_in,
-                                                       f32x4* p_out, f32x4* s_pair, f32x4* s_quad) {
+                                                       f32x4* p_out, f32x4* s_pair, f32x4* s_quad, f32x4* s_id) {
   typedef f16 f16x16 __attribute__((ext_vector_type(16)));
   typedef f16 f16x2 __attribute__((ext_vector_type(2)));
   typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -289,6 +375,18 @@ __global__ __launch_bounds__(64) void selfcheck_kernel(const f16x8* in_a, const 
   s_pair[lane] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, even, s_in[lane], 0, 0, 0);
   const f16x16 bb = __builtin_shufflevector(odd, even, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
   s_quad[lane] = __builtin_amdgcn_smfmac_f32_16x16x64_f16(sel4, bb, s_in[lane], idx, 0, 0);
+  const f16x4 id16 = identity_16x16x16(lane), id4 = identity_4x4x4(lane);
+  f32x4 t16 = s_in[lane], t4 = s_in[lane];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    f16x4 x;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[r] = (f16)p[c][r];
+    t16 = __builtin_amdgcn_mfma_f32_16x16x16f16(id16, x, t16, 0, 0, 0);
+    t4 = __builtin_amdgcn_mfma_f32_4x4x4f16(id4, x, t4, 0, 0, 0);
+  }
+  s_id[lane] = t16;
+  s_id[64 + lane] = t4;
 }
 
 // Host side of part 0.  Integer-valued inputs keep every partial and sum
@@ -299,7 +397,7 @@ __global__ __launch_bounds__(64) void selfcheck_kernel(const f16x8* in_a, const 
 // different association).  Returns the number of mismatches.
 int selfcheck(bool integers, unsigned seed, double* worst_ulp) {
   std::vector<f16x8> ha(4 * 64), hb(4 * 64);
-  std::vector<f32x4> hs(64), hp(4 * 64), hpair(64), hquad(64);
+  std::vector<f32x4> hs(64), hp(4 * 64), hpair(64), hquad(64), hid(128);
   unsigned st = seed;
   auto rnd = [&]() {  // xorshift32
     st ^= st << 13;
@@ -321,24 +419,26 @@ int selfcheck(bool integers, unsigned seed, double* worst_ulp) {
   for (int i = 0; i < 64; ++i)
     for (int r = 0; r < 4; ++r) hs[i][r] = integers ? (float)((int)(rnd() % 2001) - 1000) : (float)(100.0 * gauss());
   f16x8 *da, *db;
-  f32x4 *ds, *dp, *dpair, *dquad;
+  f32x4 *ds, *dp, *dpair, *dquad, *did;
   CHECK(hipMalloc(&da, ha.size() * sizeof(f16x8)));
   CHECK(hipMalloc(&db, hb.size() * sizeof(f16x8)));
   CHECK(hipMalloc(&ds, hs.size() * sizeof(f32x4)));
   CHECK(hipMalloc(&dp, hp.size() * sizeof(f32x4)));
   CHECK(hipMalloc(&dpair, 64 * sizeof(f32x4)));
   CHECK(hipMalloc(&dquad, 64 * sizeof(f32x4)));
+  CHECK(hipMalloc(&did, 128 * sizeof(f32x4)));
   CHECK(hipMemcpy(da, ha.data(), ha.size() * sizeof(f16x8), hipMemcpyHostToDevice));
   CHECK(hipMemcpy(db, hb.data(), hb.size() * sizeof(f16x8), hipMemcpyHostToDevice));
   CHECK(hipMemcpy(ds, hs.data(), hs.size() * sizeof(f32x4), hipMemcpyHostToDevice));
-  hipLaunchKernelGGL(selfcheck_kernel, dim3(1), dim3(64), 0, 0, da, db, ds, dp, dpair, dquad);
+  hipLaunchKernelGGL(selfcheck_kernel, dim3(1), dim3(64), 0, 0, da, db, ds, dp, dpair, dquad, did);
   CHECK(hipGetLastError());
   CHECK(hipDeviceSynchronize());
   CHECK(hipMemcpy(hp.data(), dp, hp.size() * sizeof(f32x4), hipMemcpyDeviceToHost));
   CHECK(hipMemcpy(hpair.data(), dpair, 64 * sizeof(f32x4), hipMemcpyDeviceToHost));
   CHECK(hipMemcpy(hquad.data(), dquad, 64 * sizeof(f32x4), hipMemcpyDeviceToHost));
-  for (void* q : {(void*)da, (void*)db, (void*)ds, (void*)dp, (void*)dpair, (void*)dquad}) CHECK(hipFree(q));
-  int bad = 0, rounded = 0;
+  CHECK(hipMemcpy(hid.data(), did, 128 * sizeof(f32x4), hipMemcpyDeviceToHost));
+  for (void* q : {(void*)da, (void*)db, (void*)ds, (void*)dp, (void*)dpair, (void*)dquad, (void*)did}) CHECK(hipFree(q));
+  int bad = 0, rounded = 0, bad_id = 0;
   *worst_ulp = 0;
   for (int l = 0; l < 64; ++l)
     for (int r = 0; r < 4; ++r) {
@@ -347,6 +447,9 @@ int selfcheck(bool integers, unsigned seed, double* worst_ulp) {
         h[c] = (double)(float)(f16)hp[c * 64 + l][r];  // RNE to binary16, as v_cvt_pk_f16_f32
         rounded += h[c] != (double)hp[c * 64 + l][r];
       }
+      // the identity sums: two FP32 additions in chunk order, bit for bit
+      const float seq = (hs[l][r] + (float)h[0]) + (float)h[1];
+      bad_id += (hid[l][r] != seq) + (hid[64 + l][r] != seq);
       const double pair = (double)hs[l][r] + h[0] + h[1];
       const double quad = pair + h[2] + h[3];
       for (int which = 0; which < 2; ++which) {
@@ -364,7 +467,9 @@ int selfcheck(bool integers, unsigned seed, double* worst_ulp) {
   }
   std::printf("self-check (%s inputs): %d of 512 sums off, %d of 1024 partials rounded to binary16, "
               "worst %.2f ulp\n", integers ? "integer" : "N(0,1)", bad, rounded, *worst_ulp);
-  return bad;
+  std::printf("identity-sum check (%s inputs): %d of 512 sums off (16x16x16 and 4x4x4 forms, exact)\n",
+              integers ? "integer" : "N(0,1)", bad_id);
+  return bad + bad_id;
 }
 
 struct Bufs {
@@ -442,6 +547,14 @@ int main() {
     c[5] = measure(epilogue_kernel<5>, b, 16, w);
     c[6] = measure(epilogue_kernel<6>, b, 16, w);
     for (int i = 0; i < 7; ++i) std::printf("  %-33s %8.2f  %.3f\n", names[i], c[i], 32.0 / c[i]);
+    std::printf("part 3: cycles per MFMA (16 independent accumulators)\n");
+    std::printf("  %-33s %8.2f\n", "v_mfma_f32_16x16x32_f16", measure(mfma_rate_kernel<0>, b, 16, w));
+    std::printf("  %-33s %8.2f\n", "v_mfma_f32_16x16x16_f16", measure(mfma_rate_kernel<1>, b, 16, w));
+    std::printf("  %-33s %8.2f\n", "v_mfma_f32_4x4x4_16b_f16", measure(mfma_rate_kernel<2>, b, 16, w));
+    std::printf("  chunk-pair epilogues with lane-local identity sums; cycles per block step, fraction of peak\n");
+    const double e7 = measure(epilogue_kernel<7>, b, 8, w), e8 = measure(epilogue_kernel<8>, b, 8, w);
+    std::printf("  %-33s %8.2f  %.3f\n", "cvt_pk x4 + 2 x 16x16x16 identity", e7, 32.0 / e7);
+    std::printf("  %-33s %8.2f  %.3f\n", "cvt_pk x4 + 2 x 4x4x4 identity", e8, 32.0 / e8);
     CHECK(hipFree(b.out));
     CHECK(hipFree(b.cyc));
   }
