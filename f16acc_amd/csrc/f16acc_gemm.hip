@@ -129,7 +129,8 @@ static_assert(sizeof(RedoList) == F16ACC_WS_HEADER, "the list fills the workspac
 __device__ __forceinline__ int load_agent(const int* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void store_agent(int* p, int v) {
+// (unused in the builds with the redo compiled out)
+[[maybe_unused]] __device__ __forceinline__ void store_agent(int* p, int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
