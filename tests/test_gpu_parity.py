@@ -1172,6 +1172,63 @@ def test_randomized_shapes_layouts_and_tiles_match_oracle(case):
         assert torch.equal(c.cpu()[finite], ref[finite])
 
 
+def _twin(t):
+    """The GPU copy of a CPU view: the whole base storage copied, the same
+    strides and offset."""
+    base = t.as_strided((t.untyped_storage().nbytes() // 2,), (1,), 0)
+    return base.cuda().as_strided(t.shape, t.stride(), t.storage_offset())
+
+
+def _check_against_oracle(c, ref, what):
+    finite = torch.isfinite(ref)
+    assert torch.equal(torch.isfinite(c.cpu()), finite), what
+    if bool(finite.any()) and float(ref[finite].abs().max()) > 0:
+        err = (c.cpu()[finite].double() - ref[finite].double()).abs().max() / ref[finite].double().abs().max()
+        assert err < TOL, (what, float(err))
+    else:
+        assert torch.equal(c.cpu()[finite], ref[finite]), what
+
+
+@pytest.mark.parametrize("case", range(40))
+def test_randomized_long_k_on_few_tiles_through_mm_and_bias(case):
+    """Seeded random problems with few tiles and a long K (M, N in 1..520,
+    K in 1024..6000: split-K plans and the K-group tiles), any operand layout
+    (b mostly K-contiguous, as the K-group tiles need), fp16 or fp32 output,
+    chunked or not, some tiles overflowing: the single grid with tile flags
+    (forced tile or the table's) against the oracle; mm itself (its
+    workspace: split-K partials, the deferred redo list) against the oracle
+    too; and for fp16 output the fused bias equal to mm + bias bit for bit."""
+    import random
+
+    r = random.Random(4000 + case)
+    M, N, K = r.randint(1, 520), r.randint(1, 520), r.randint(1024, 6000)
+    kinds = ["contiguous", "transposed", "strided", "offset", "broadcast", "window"]
+    ka = r.choice(kinds)
+    kb = "transposed" if r.random() < 0.7 else r.choice(kinds)
+    a = _random_operand(None, M, K, ka, 8000 + case)
+    b = _random_operand(None, K, N, kb, 9000 + case)
+    if r.random() < 0.3 and ka not in ("broadcast", "window") and kb not in ("broadcast", "window"):
+        i0, j0 = r.randrange(M), r.randrange(N)
+        a[i0 : i0 + 4, :] = 60.0
+        b[:, j0 : j0 + 4] = 60.0
+    out_dtype = r.choice([torch.float16, torch.float32])
+    chunked = r.random() < 0.85
+    tile = r.choice([None, None, None] + list(_lib.TILES))
+    what = (case, M, N, K, ka, kb, out_dtype, chunked, tile)
+    ga, gb = _twin(a), _twin(b)
+    cfg = tile_config(ga, gb, tile)
+    c, flags = mm_flags(ga, gb, out_dtype, chunked, tile=tile)
+    ref, rflags = oracle(a, b, out_dtype, cfg, chunked=chunked)
+    assert torch.equal(flags.cpu(), rflags), what
+    _check_against_oracle(c, ref, what)
+    _check_against_oracle(f16acc.mm(ga, gb, out_dtype, chunked=chunked), ref, what)
+    if out_dtype == torch.float16 and chunked:
+        bias = rnd((N,), 10000 + case, 0.1).cuda()
+        want = f16acc.mm(ga, gb)
+        want += bias
+        assert torch.equal(f16acc.kernel.mm_bias(ga, gb, bias), want), what
+
+
 @pytest.mark.parametrize("b_layout", ["w.t()", "row-major"])
 def test_ragged_round_row_cut_equals_single_grid(b_layout):
     """A tall problem (8960 x 2048 x 1536: 35 x 8 tiles of 256x256 for 256
