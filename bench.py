@@ -252,7 +252,7 @@ def tile_calls(names, calls):
 LLM_MODELS = (("llama2-7b", 4096, 4096, 11008), ("llama3-8b", 4096, 1024, 14336), ("qwen2.5-7b", 3584, 512, 18944))
 
 
-def table_check(tokens=(256, 1024, 4096), rounds=3):
+def table_check(tokens=(256, 1024, 4096), rounds=4):
     """The per-shape table against every forced tile on the layer GEMMs of
     LLM_MODELS at several token counts (x [M, K] @ w.t(), w [N, K] ~ N(0, 0.02),
     fp16 out, chunked): per-call times in settled bursts (median of interleaved
@@ -274,9 +274,16 @@ def table_check(tokens=(256, 1024, 4096), rounds=3):
                 ops = {"table": lambda: f16acc_amd.mm(a, b)}
                 ops.update({tile: (lambda x=tile: mm_tile(a, b, x)) for tile in tiles})
                 runs = {k: [] for k in ops}
-                for _ in range(rounds):  # interleaved, so clock drift falls on all alike
-                    for k, op in ops.items():
-                        runs[k].append(settled_time(op))
+                names = list(ops)
+                for r in range(rounds):
+                    # interleaved, so clock drift falls on all alike; the order
+                    # rotates and reverses from round to round, since the op
+                    # timed first after another shape runs ~2-5 % slow (kernel
+                    # times keep falling for tens of ms after a switch)
+                    shift = r * len(names) // rounds
+                    order = names[shift:] + names[:shift]
+                    for k in (order[::-1] if r % 2 else order):
+                        runs[k].append(settled_time(ops[k]))
                 t = {k: statistics.median(v) for k, v in runs.items()}
                 best = min(tiles, key=lambda k: t[k])
                 ratios.append(t[best] / t["table"])

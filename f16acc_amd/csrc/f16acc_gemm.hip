@@ -1939,6 +1939,31 @@ constexpr double kSplitCost = 1.08;
 constexpr int kMinSplitStages = 16;
 constexpr int kMaxSplits = 16;
 
+// Whether a K split in `splits` pays for itself, in seconds: a split's
+// fixed cost (the FP32 partials written and read back, at ~8 TB/s where
+// they stay in the L2 and MALL, and the finishing launch, ~3 us) against
+// what it saves.  Unsplit, a grid of fewer tiles than CUs runs one
+// workgroup per CU, which takes kLoneSecPerK per K element (measured, one
+// workgroup alone on its CU); split, the busiest CU runs n = ceil(tiles x
+// splits / CUs) workgroups of K / splits: at two per CU (128x128) each runs
+// at 1 / kLoneSpeedup of the lone speed, a single-slot tile runs them one
+// after another.  Fitted to 1024 x 3584 x {3584, 18944} w.t() on 224
+// 128x128 tiles (unsplit 42.8 and 205.2 us, split in two 46.6 and 185.0:
+// split ~ 0.85 x unsplit + ~10 us), and it keeps llama-3-8B gate/up at 256
+// tokens (224 tiles, K = 4096) unsplit, 48.7 against 50.2 us split; grids of
+// a quarter of the CUs or fewer still split (llama-2-7B down at 256 tokens,
+// 64 tiles in eight: 45.5 against 114.1 us).
+constexpr double kLoneSpeedup = 1.7;
+inline double lone_sec_per_k(int tile) { return tile == F16ACC_TILE_128x128 ? 11.5e-9 : 17.5e-9; }
+inline bool split_pays(int tile, int64_t tiles, int64_t splits, int64_t K, int cus) {
+  const TileInfo& t = kTiles[tile];
+  const double lone = lone_sec_per_k(tile) * (double)K;
+  const int64_t n = cdiv(tiles * splits, cus);
+  const double busy = t.per_cu >= 2 ? (n <= 1 ? 1.0 : n / 2.0 * kLoneSpeedup) : (double)n;
+  const double fixed = 3e-6 + (double)tiles * splits * t.bm * t.bn * sizeof(float) * 2 / 8e12;
+  return lone / (double)splits * busy + fixed < lone;
+}
+
 // The split count plan_split uses for a tile with `tiles` tiles, `slots`
 // workgroup slots and nsteps LDS stages: as many splits as fill the slots,
 // each split keeping at least kMinSplitStages stages, at most kMaxSplits.
@@ -2052,9 +2077,13 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
     double est_best = (double)t.bm * t.bn * t.per_cu / kTileRate[best];
     const int64_t splits =
         best == F16ACC_TILE_256x256 || best == F16ACC_TILE_256x288 ? 1 : split_count(tiles, slots, cdiv(K, kStageK));
-    if (splits > 1) {
+    if (splits > 1 && split_pays(best, tiles, splits, K, cus)) {
       const double est_split = (double)cdiv(tiles * splits, slots) * est_best / splits * kSplitCost;
       if (est_split < est_best) est_best = est_split;
+    } else if (splits > 1) {
+      // the split does not pay (plan_split keeps the grid whole): its one
+      // workgroup per CU runs the round kLoneSpeedup times as fast
+      est_best /= t.per_cu >= 2 ? kLoneSpeedup : 1.0;
     }
     const double est_small =
         (double)cdiv(stiles, (int64_t)cus * s.per_cu) * s.bm * s.bn * s.per_cu / kSmallTileRate;
@@ -2247,7 +2276,7 @@ inline SplitPlan plan_split(const Choice& ch, int64_t M, int64_t N, int64_t K, i
   const int64_t slots = (int64_t)cus * t.per_cu;
   const int64_t nsteps = cdiv(K, kStageK);
   const int64_t splits = split_count(tiles, slots, nsteps);
-  if (splits < 2) return sp;
+  if (splits < 2 || !split_pays(ch.tile, tiles, splits, K, cus)) return sp;
   const int64_t steps_per = cdiv(nsteps, splits);
   sp.splits = (int)splits;
   sp.kps = steps_per * kStageK;

@@ -352,6 +352,33 @@ def test_k_split_only_where_cus_would_idle():
         assert (n.value > 0) == split, (M, N, K, b_kc)
 
 
+def _pick_and_splits(M, N, K):
+    """(tile, splits) the library plans for x [M, K] @ w.t(), w [N, K]."""
+    tid, bm, bn, fam, thr = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    tm, tn = ctypes.c_int64(), ctypes.c_int64()
+    _lib.check(_lib.tile_config(M, N, K, K, 1, 1, K, 0, 0, -1, ctypes.byref(tid), ctypes.byref(bm), ctypes.byref(bn),
+                                ctypes.byref(tm), ctypes.byref(tn), ctypes.byref(fam), ctypes.byref(thr)))
+    n = ctypes.c_size_t()
+    _lib.check(_lib.workspace_size(M, N, K, K, 1, 1, K, 0, 0, ctypes.byref(n)))
+    part = max(n.value - _lib.WS_HEADER, 0)
+    return _lib.TILES[tid.value], part // (tm.value * tn.value * bm.value * bn.value * 4) if part else 1
+
+
+@pytest.mark.parametrize("M, N, K, tile, splits", [
+    (1024, 3584, 3584, "128x128", 1),    # Qwen2.5-7B q/o, 1024 tokens: 224 tiles, short K: 42.8 us whole, 46.6 split
+    (256, 14336, 4096, "128x128", 1),    # llama-3-8B gate/up, 256 tokens: 224 tiles: 48.7 us whole, 50.2 split
+    (1024, 3584, 18944, "128x128", 2),   # Qwen2.5-7B down, 1024 tokens: 224 tiles, long K: 185.0 us split, 205.2 whole
+    (256, 4096, 11008, "128x128", 8),    # llama-2-7B down, 256 tokens: 64 tiles: 45.5 us split, 114.1 whole
+    (2049, 1537, 8968, "128x128", 2),    # the packed odd config: 221 tiles, long K
+])
+def test_k_split_only_where_it_pays(M, N, K, tile, splits):
+    """A grid with fewer tiles than CUs is split along K only when the time
+    it saves exceeds the split's fixed cost (the FP32 partials' traffic and
+    the finishing launch): not at 224 of 256 CUs with a short K, yes with a
+    long K or a grid of a quarter of the CUs."""
+    assert _pick_and_splits(M, N, K) == (tile, splits)
+
+
 def test_workspace_holds_the_redo_list_where_it_is_deferred():
     """f16acc_workspace_size: one round of 256x256 tiles (4096^3) needs the
     header alone (its flagged tiles are listed and redone by a second launch);
