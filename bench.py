@@ -137,8 +137,8 @@ def read_traffic(workload):
         return None
 
 
-# Host threads the CPU baseline uses: a one-GPU job on the GPU box gets a
-# 16-core share of its host, whatever os.cpu_count() reports there.
+# Host threads the CPU baseline uses: a one-GPU job on an eight-GPU MI355X
+# node gets a 16-core share of its host, whatever os.cpu_count() reports.
 CPU_SHARE = 16
 
 
@@ -182,7 +182,7 @@ def cpu_baseline(a, b, out_dtype, budget_s=20.0):
     t1 = statistics.median(t1)
     info = {"value": 2.0 * M * N * K / t / 1e12, "unit": "TFLOPS", "cores": threads, "kind": "port",
             "host_cpus": host, "cpu_model": cpu_model(),
-            "thread_cap": f"{CPU_SHARE}: the GPU box's CPU share for one GPU",
+            "thread_cap": f"{CPU_SHARE}: one GPU's share of the node's host CPUs",
             "sample": f"the full {M}x{N}x{K} GEMM (oracle/chunk32.py, torch CPU, {threads} threads), "
                       f"median of {len(times)} run(s), {t:.2f} s each",
             "gemm1024_f32": {"value": round(2.0 * 1024 ** 3 / t1 / 1e12, 4), "unit": "TFLOPS",
