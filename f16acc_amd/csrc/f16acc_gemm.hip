@@ -1917,6 +1917,11 @@ inline void canon_strides(int64_t M, int64_t N, int64_t K, int64_t* sam, int64_t
 // 256x256 reads the least LDS per MFMA (64x128 per wave) and wins whenever
 // its tiles fill the machine; smaller tiles win on shapes with few tiles.
 constexpr double kTileRate[4] = {1.00, 0.87, 0.87, 0.89};
+// The rate of any tile the table weighs: 256x288 (a ninth column block per
+// wave of 256x256) runs at 256x256's rate.
+inline double tile_rate(int id) {
+  return id >= F16ACC_TILE_256x256 && id <= F16ACC_TILE_128x128 ? kTileRate[id] : kTileRate[F16ACC_TILE_256x256];
+}
 
 // The per-shape table: the fast tile with the smallest estimated time.
 // Ties keep the larger tile.
@@ -2074,7 +2079,7 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
     }
     const TileInfo& s = kTiles[F16ACC_TILE_64x64];
     const int64_t stiles = cdiv(M, s.bm) * cdiv(N, s.bn);
-    double est_best = (double)t.bm * t.bn * t.per_cu / kTileRate[best];
+    double est_best = (double)t.bm * t.bn * t.per_cu / tile_rate(best);
     const int64_t splits =
         best == F16ACC_TILE_256x256 || best == F16ACC_TILE_256x288 ? 1 : split_count(tiles, slots, cdiv(K, kStageK));
     if (splits > 1 && split_pays(best, tiles, splits, K, cus)) {

@@ -370,12 +370,17 @@ def _pick_and_splits(M, N, K):
     (1024, 3584, 18944, "128x128", 2),   # Qwen2.5-7B down, 1024 tokens: 224 tiles, long K: 185.0 us split, 205.2 whole
     (256, 4096, 11008, "128x128", 8),    # llama-2-7B down, 256 tokens: 64 tiles: 45.5 us split, 114.1 whole
     (2049, 1537, 8968, "128x128", 2),    # the packed odd config: 221 tiles, long K
+    (1536, 11008, 1536, "256x288", 1),   # 234 tiles of 256x288, one round: 64.8 us, 88.7 on 64x64
+    (1536, 11008, 4096, "256x288", 1),   # 153.4 us, 221.8 on 64x64
 ])
 def test_k_split_only_where_it_pays(M, N, K, tile, splits):
     """A grid with fewer tiles than CUs is split along K only when the time
     it saves exceeds the split's fixed cost (the FP32 partials' traffic and
     the finishing launch): not at 224 of 256 CUs with a short K, yes with a
-    long K or a grid of a quarter of the CUs."""
+    long K or a grid of a quarter of the CUs.  A 256x288 grid of one partial
+    round is weighed against 64x64 at 256x256's rate (the table read past its
+    four-entry rate array there, a fault the host sanitizer build found, and
+    sent these shapes to 64x64)."""
     assert _pick_and_splits(M, N, K) == (tile, splits)
 
 
