@@ -29,7 +29,8 @@ them one tile per workgroup; --workload
 overflow_split_redo times the overflow stress workload against a build that
 redoes flagged tiles in a split-K pass instead of in the same workgroup;
 --workload table_check times the per-shape table against every forced tile on
-llama-2-7B, llama-3-8B and Qwen2.5-7B layer shapes; --tile-calls runs every tile
+llama-2-7B, llama-3-8B and Qwen2.5-7B layer shapes; --workload small_grid_check
+times its small-grid picks (K-group tiles, 64x64) against the other candidates; --tile-calls runs every tile
 untimed for rocprofv3 counter passes.
 """
 
@@ -296,6 +297,51 @@ def table_check(tokens=(256, 1024, 4096), rounds=4):
     print(json.dumps({"shapes": len(ratios), "table_at_least_as_fast": sum(r >= 0.999 for r in ratios),
                       "within_5pct_of_best_forced": sum(r >= 0.95 for r in ratios),
                       "worst_best_forced_over_table": round(min(ratios), 3)}), flush=True)
+
+
+def small_grid_check(rounds=3):
+    """The table's pick against 128x96 in two K groups, 64x32 in four, 64x64
+    and 128x128 (each forced) on grids that leave CUs idle: x [M, K] @ w.t()
+    over M 256..4096, N 256..5120, K 1024..8192 and a second grid of other
+    extents, wherever the table picks a K-group tile or 64x64 (the region of
+    its small-grid rules).  Per-call times in settled bursts, median of
+    rounds whose order rotates; one JSON line per shape and a summary."""
+    import itertools
+
+    import f16acc_amd
+    from f16acc_amd.kernel import mm_tile, tile_config
+
+    cands = ["128x96k2", "64x32k4", "64x64", "128x128"]
+    grid = list(itertools.product((256, 512, 1024, 1536, 2048, 3072, 4096), (256, 512, 1024, 1536, 2816, 5120),
+                                  (1024, 1536, 4096, 8192)))
+    grid += list(itertools.product((384, 768, 1280, 2560), (384, 768, 1280, 2048), (1280, 2048, 2816, 5120)))
+    ratios = []
+    for M, N, K in grid:
+        g = torch.Generator().manual_seed(0)
+        a = torch.randn(M, K, generator=g).half().cuda()
+        b = (torch.randn(N, K, generator=g) * 0.02).half().cuda().t()
+        pick = tile_config(a, b)["tile"]
+        if pick not in ("128x96k2", "64x32k4", "64x64"):
+            continue
+        ops = {"table": lambda: f16acc_amd.mm(a, b)}
+        ops.update({t: (lambda x=t: mm_tile(a, b, x)) for t in cands})
+        names = list(ops)
+        runs = {k: [] for k in ops}
+        for r in range(rounds):
+            shift = r * len(names) // rounds
+            order = names[shift:] + names[:shift]
+            for k in (order[::-1] if r % 2 else order):
+                runs[k].append(settled_time(ops[k], burst_ms=20.0))
+        t = {k: statistics.median(v) for k, v in runs.items()}
+        best = min(cands, key=lambda k: t[k])
+        ratios.append(t[best] / t[pick])
+        print(json.dumps({"M": M, "N": N, "K": K, "pick": pick, "pick_forced_us": round(t[pick] * 1e6, 2),
+                          "best_forced": best, "best_forced_over_pick": round(ratios[-1], 3),
+                          **{k: round(v * 1e6, 2) for k, v in t.items()}}), flush=True)
+        del a, b
+    print(json.dumps({"shapes": len(ratios), "pick_is_best": sum(r >= 0.999 for r in ratios),
+                      "within_5pct": sum(r >= 0.95 for r in ratios), "within_10pct": sum(r >= 0.90 for r in ratios),
+                      "worst_best_forced_over_pick": round(min(ratios), 3)}), flush=True)
 
 
 def settled_time(op, burst_ms=40.0):
@@ -751,7 +797,7 @@ def main():
     ap.add_argument("--workload", default="gemm4096",
                     choices=sorted(WORKLOADS) + ["copy", "overflow", "overflow_split_redo", "qwen2_prefill",
                                                  "redo_overhead", "persistent_ab", "shapes",
-                                                 "table_check"])
+                                                 "table_check", "small_grid_check"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and oracle comparison")
     ap.add_argument("--preheat", type=float, default=PREHEAT_S,
                     help="seconds of back-to-back calls before the warm-up steps (0 for counter runs)")
@@ -772,6 +818,8 @@ def main():
         return copy_reference(args.steps, args.warmup)
     if args.workload == "table_check":
         return table_check()
+    if args.workload == "small_grid_check":
+        return small_grid_check()
     if args.workload == "shapes":
         return shapes_report(list(WORKLOADS))
     if args.workload == "overflow":

@@ -2060,7 +2060,23 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
     if (kc) {
       const int64_t n2 = cdiv(M, kTiles[F16ACC_TILE_128x96_K2].bm) * cdiv(N, kTiles[F16ACC_TILE_128x96_K2].bn);
       const int64_t n4 = cdiv(M, kTiles[F16ACC_TILE_64x32_K4].bm) * cdiv(N, kTiles[F16ACC_TILE_64x32_K4].bn);
+      const TileInfo& q = kTiles[F16ACC_TILE_64x64];
+      const int64_t n64 = cdiv(M, q.bm) * cdiv(N, q.bn);
+      const double est64 = (double)cdiv(n64, (int64_t)cus * q.per_cu) * q.bm * q.bn * q.per_cu / kSmallTileRate;
       const int kid = n2 <= cus && 2 * n2 > cus ? F16ACC_TILE_128x96_K2 : n4 <= cus ? F16ACC_TILE_64x32_K4 : -1;
+      // A round of 128x96 tiles that leaves CUs idle loses to 64x64 whenever
+      // 64x64 runs at most two workgroups per CU: 1536 x 1024, 2048 x 1024,
+      // 3072 x 512 and 4096 x 512 (w.t(), 132-192 tiles of 128x96, 384-512 of
+      // 64x64) ran 2-35 % faster on 64x64 at every K from 1024 to 8192, and so
+      // did 768 x 2048, 1280 x 1280 and 2560 x 768 at K = 1280 to 5120 (up to
+      // 32 %; one case -1.8 %) (Qwen2.5-7B k/v at 4096 tokens: 30.3 against
+      // 31.6 us).  At three or more per CU 128x96 keeps the lead (1536 x
+      // 1536: 34.1 against 37.9 us at K = 4096; Qwen2.5-1.5B q/o and down,
+      // 256 tiles of 128x96).
+      if (kid == F16ACC_TILE_128x96_K2 && n64 <= 2 * (int64_t)cus) {
+        if (est) *est = est64;
+        return F16ACC_TILE_64x64;
+      }
       if (kid >= 0) {
         if (est) {
           choose_tile(M, N, K, cus, est, false);
@@ -2069,6 +2085,16 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
         return kid;
       }
       if (n4 <= 2 * (int64_t)cus) {
+        // two rounds of 64x32 lose to one round of 64x64 at a short K: 1024 x
+        // 1024, 2048 x 512, 4096 x 256, 1536 x 512, 768 x 1280 and 2560 x 384
+        // (w.t()) ran 7-21 % faster on 64x64 at K = 1024, 1280 and 1536; at
+        // K = 2048 it won on some of them and lost on others (-9 to +16 %),
+        // at 2816 and 4096 64x32 wins by 12-15 % (Qwen2.5-7B q/o at 256
+        // tokens, K = 3584, stays on 64x32: 22.6 against 28.0 us)
+        if (n64 <= cus && K < 2048) {
+          if (est) *est = est64;
+          return F16ACC_TILE_64x64;
+        }
         double other = 0;
         choose_tile(M, N, K, cus, &other, false);
         if (2 * kKGroup4Round <= other * 1.001) {

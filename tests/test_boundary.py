@@ -136,6 +136,11 @@ class _Fake:
     (256, 4096, 11008, (11008, 1), (1, 11008), "fast", "128x128"), # llama-2-7B down, 256 tokens: split in eight
     (256, 11008, 4096, (4096, 1), (1, 4096), "fast", "128x96k2"),  # llama-2-7B gate/up, 256 tokens: 230 tiles
     (2048, 1536, 8960, (8960, 1), (1, 8960), "fast", "128x96k2"),  # Qwen down: K groups, no second launch
+    (4096, 512, 3584, (3584, 1), (1, 3584), "fast", "64x64"),      # Qwen2.5-7B k/v, 4096 tokens: 192 128x96 tiles lose
+    (1536, 1024, 1024, (1024, 1), (1, 1024), "fast", "64x64"),     # to 512 (384) of 64x64, 2 per CU: 30.3 / 10.3 us
+    (1536, 1536, 4096, (4096, 1), (1, 4096), "fast", "128x96k2"),  # 576 64x64 tiles (3 on some CUs): 128x96 keeps it
+    (1024, 1024, 1536, (1536, 1), (1, 1536), "fast", "64x64"),     # two rounds of 64x32 at K 1536: 64x64 (11.2 vs 12.7)
+    (1024, 1024, 2048, (2048, 1), (1, 2048), "fast", "64x32k4"),   # ... from K 2048 64x32 stays
     (2048, 1536, 8960, (8960, 1), (1536, 1), "fast", "128x128"),   # row-major b: 128x128 split in two
     (128, 1536, 1536, (1536, 1), (1536, 1), "fast", "64x64"),      # 128 rows, row-major b
     (2049, 1537, 8961, (8961, 1), (1, 8961), "fast", "128x128"),   # rows not 16-byte aligned: packed first
