@@ -30,7 +30,8 @@ overflow_split_redo times the overflow stress workload against a build that
 redoes flagged tiles in a split-K pass instead of in the same workgroup;
 --workload table_check times the per-shape table against every forced tile on
 llama-2-7B, llama-3-8B and Qwen2.5-7B layer shapes; --workload small_grid_check
-times its small-grid picks (K-group tiles, 64x64) against the other candidates; --tile-calls runs every tile
+times its small-grid picks (K-group tiles, 64x64) against the other candidates,
+--workload large_grid_check its picks on grids of a round or more; --tile-calls runs every tile
 untimed for rocprofv3 counter passes.
 """
 
@@ -296,6 +297,51 @@ def table_check(tokens=(256, 1024, 4096), rounds=4):
                 del a, b
     print(json.dumps({"shapes": len(ratios), "table_at_least_as_fast": sum(r >= 0.999 for r in ratios),
                       "within_5pct_of_best_forced": sum(r >= 0.95 for r in ratios),
+                      "worst_best_forced_over_table": round(min(ratios), 3)}), flush=True)
+
+
+def large_grid_check(rounds=3):
+    """The table's pick against every fast tile (forced) on grids of at
+    least one round: x [M, K] @ w.t() over M 1024..8192, N 1024..16384,
+    K 1024 and 4096, wherever the table picks a 256-row or 128x128 tile.
+    mm as shipped is timed too ("table": with the ragged-round cut and the
+    deferred redo launch where it plans them).  Per-call times in settled
+    bursts, median of rounds whose order rotates; one JSON line per shape
+    and a summary."""
+    import itertools
+
+    import f16acc_amd
+    from f16acc_amd import _lib
+    from f16acc_amd.kernel import mm_tile, tile_config
+
+    cands = [t for t in _lib.TILES if t not in ("generic", "128x96k2", "64x32k4")]
+    ratios = []
+    for M, N, K in itertools.product((1024, 2048, 3072, 4096, 6144, 8192), (1024, 3072, 5120, 9216, 16384),
+                                     (1024, 4096)):
+        g = torch.Generator().manual_seed(0)
+        a = torch.randn(M, K, generator=g).half().cuda()
+        b = (torch.randn(N, K, generator=g) * 0.02).half().cuda().t()
+        pick = tile_config(a, b)["tile"]
+        if pick not in ("256x256", "256x288", "256x128", "128x256", "128x128"):
+            continue
+        ops = {"table": lambda: f16acc_amd.mm(a, b)}
+        ops.update({t: (lambda x=t: mm_tile(a, b, x)) for t in cands})
+        names = list(ops)
+        runs = {k: [] for k in ops}
+        for r in range(rounds):
+            shift = r * len(names) // rounds
+            order = names[shift:] + names[:shift]
+            for k in (order[::-1] if r % 2 else order):
+                runs[k].append(settled_time(ops[k], burst_ms=25.0))
+        t = {k: statistics.median(v) for k, v in runs.items()}
+        best = min(cands, key=lambda k: t[k])
+        ratios.append(t[best] / t["table"])
+        print(json.dumps({"M": M, "N": N, "K": K, "pick": pick, "table_us": round(t["table"] * 1e6, 1),
+                          "best_forced": best, "best_forced_over_table": round(ratios[-1], 3),
+                          **{k: round(v * 1e6, 1) for k, v in t.items() if k != "table"}}), flush=True)
+        del a, b
+    print(json.dumps({"shapes": len(ratios), "table_at_least_as_fast": sum(r >= 0.999 for r in ratios),
+                      "within_5pct": sum(r >= 0.95 for r in ratios), "within_10pct": sum(r >= 0.90 for r in ratios),
                       "worst_best_forced_over_table": round(min(ratios), 3)}), flush=True)
 
 
@@ -797,7 +843,7 @@ def main():
     ap.add_argument("--workload", default="gemm4096",
                     choices=sorted(WORKLOADS) + ["copy", "overflow", "overflow_split_redo", "qwen2_prefill",
                                                  "redo_overhead", "persistent_ab", "shapes",
-                                                 "table_check", "small_grid_check"])
+                                                 "table_check", "small_grid_check", "large_grid_check"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and oracle comparison")
     ap.add_argument("--preheat", type=float, default=PREHEAT_S,
                     help="seconds of back-to-back calls before the warm-up steps (0 for counter runs)")
@@ -820,6 +866,8 @@ def main():
         return table_check()
     if args.workload == "small_grid_check":
         return small_grid_check()
+    if args.workload == "large_grid_check":
+        return large_grid_check()
     if args.workload == "shapes":
         return shapes_report(list(WORKLOADS))
     if args.workload == "overflow":

@@ -1993,6 +1993,42 @@ inline double rounds_of(int64_t n, int cus, double full) {
   return (double)(n / cus) * full + (r ? full * (0.73 + 0.27 * f * f * f) : 0.0);
 }
 
+// Time of n tiles of a two-per-CU tile (128x128), each costing `tile` in the
+// units of kTileRate at full occupancy: a last round that puts at most one
+// workgroup on each CU runs each alone, kLoneSpeedup times as fast as a
+// paired one, not twice.  4096 x 3072 (768 tiles of 128x128: a paired round
+// and a lone one, against 192 tiles of 256x256 in three quarters of a round)
+// ran 128.8 us on 128x128 and 120.7 on 256x256 at K = 4096 (37.2 and 36.2 at
+// K = 1024).  At most one round keeps ceil(n / CUs) tiles: the small-grid
+// rules weigh one workgroup per CU with measured times of their own.
+inline double rounds_paired(int64_t n, int cus, double tile) {
+  if (n <= cus) return tile;
+  const int64_t slots = 2 * (int64_t)cus, rem = n % slots;
+  return (double)(n / slots) * 2.0 * tile + (rem == 0 ? 0.0 : rem <= cus ? 2.0 * tile / kLoneSpeedup : 2.0 * tile);
+}
+
+// Time of n 64x64 tiles (four workgroups per CU) in the units of kTileRate,
+// as weighed against 128x128 on grids that leave CUs idle.  A single,
+// partial round of at most w workgroups on any CU costs a fraction of a full
+// round, fitted to forced pairs on MI355X (fp16 out, b row-major and w.t()):
+//   w = 1, 2: 0.6 -- 0.65-0.73 of 128x128 unsplit, and well under a 128x128
+//     K split in two (256 x 1024 x 2048: 13.0 us against 19.0; 1024 x 1024
+//     x 2048: 13.7 against 21.2; 4096 x 512 x 2048: 18.3 against 25.2);
+//   w = 3: 0.88 -- 0.95 of 128x128 unsplit, one workgroup per CU (3072 x
+//     1024 x 4096: 46.4 against 48.2 us; 2048 x 1536 x 3072: 35.1 against
+//     37.7), but above a 128x128 K split in two where that pays, at long K
+//     (256 x 11008 x 8192: 84.7 against 79.2; 512 x 6144 x 14336: 152.5
+//     against 137.5).
+// More rounds cost whole rounds.
+inline double rounds_64(int64_t n, int cus) {
+  const TileInfo& s = kTiles[F16ACC_TILE_64x64];
+  const double round = (double)s.bm * s.bn * s.per_cu / kSmallTileRate;
+  const int64_t slots = (int64_t)cus * s.per_cu;
+  if (n > slots) return (double)cdiv(n, slots) * round;
+  const int64_t w = cdiv(n, cus);
+  return round * (w >= s.per_cu ? 1.0 : w == 3 ? 0.88 : 0.6);
+}
+
 inline double rounds_256(int64_t n, int cus) {
   return rounds_of(n, cus, 256.0 * 256.0 / kTileRate[F16ACC_TILE_256x256]);
 }
@@ -2036,8 +2072,10 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
   for (int id = 0; id < 4; ++id) {
     const TileInfo& t = kTiles[id];
     const int64_t tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
+    const double area = (double)t.bm * t.bn / kTileRate[id];
     const double est = id == F16ACC_TILE_256x256 ? rounds_256(tiles, cus)
-                                                 : (double)cdiv(tiles, cus) * t.bm * t.bn / kTileRate[id];
+                       : t.per_cu == 2           ? rounds_paired(tiles, cus, area)
+                                                 : (double)cdiv(tiles, cus) * area;
     if (id == 0 || est < best_t * 0.999) {
       best = id;
       best_t = est;
@@ -2072,7 +2110,9 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
       // 32 %; one case -1.8 %) (Qwen2.5-7B k/v at 4096 tokens: 30.3 against
       // 31.6 us).  At three or more per CU 128x96 keeps the lead (1536 x
       // 1536: 34.1 against 37.9 us at K = 4096; Qwen2.5-1.5B q/o and down,
-      // 256 tiles of 128x96).
+      // 256 tiles of 128x96).  At K = 1024 and 1280 three per CU ran 6-10 %
+      // faster than 128x96 on two boxes and 2-18 % slower on a third, so the
+      // rule stops at two.
       if (kid == F16ACC_TILE_128x96_K2 && n64 <= 2 * (int64_t)cus) {
         if (est) *est = est64;
         return F16ACC_TILE_64x64;
@@ -2116,8 +2156,7 @@ inline int choose_tile(int64_t M, int64_t N, int64_t K, int cus, double* est = n
       // workgroup per CU runs the round kLoneSpeedup times as fast
       est_best /= t.per_cu >= 2 ? kLoneSpeedup : 1.0;
     }
-    const double est_small =
-        (double)cdiv(stiles, (int64_t)cus * s.per_cu) * s.bm * s.bn * s.per_cu / kSmallTileRate;
+    const double est_small = rounds_64(stiles, cus);
     if (est_small < est_best * 0.999) {
       if (est) *est = est_small;
       return F16ACC_TILE_64x64;
@@ -2323,8 +2362,16 @@ inline SplitPlan plan_split(const Choice& ch, int64_t M, int64_t N, int64_t K, i
 // workload (4096^3, 49 of 256 tiles flagged) it ran 222.7 us against 150.2
 // for the same shape clean.  Multi-round shapes keep the in-place redo (the
 // other workgroups go on with the next tiles meanwhile).
+//
+// Only from kDeferMinStages stages: the second launch costs ~2.3 us on
+// every call (an empty list included), which stays under 3 % of a round of
+// 256x256 tiles (~36 ns per K element) from K ~ 2500 up; shorter problems
+// keep the in-place redo, whose straggler is short with them (1024 x 9216
+// x 1024: 35.6 us per call deferred, 33.4 in place).
+constexpr int64_t kDeferMinStages = 40;
 inline bool deferred_redo(const Choice& ch, int64_t M, int64_t N, int64_t K, int cus) {
-  if (!kRedo || kSplitRedo || ch.family != F16ACC_FAMILY_FAST || ch.tile != F16ACC_TILE_256x256 || K <= 0)
+  if (!kRedo || kSplitRedo || ch.family != F16ACC_FAMILY_FAST || ch.tile != F16ACC_TILE_256x256 ||
+      cdiv(K, kStageK) < kDeferMinStages)
     return false;
   const int64_t tiles = cdiv(M, 256) * cdiv(N, 256);
   return tiles <= cus && tiles <= kRedoMax;

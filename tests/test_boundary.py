@@ -139,9 +139,15 @@ class _Fake:
     (4096, 512, 3584, (3584, 1), (1, 3584), "fast", "64x64"),      # Qwen2.5-7B k/v, 4096 tokens: 192 128x96 tiles lose
     (1536, 1024, 1024, (1024, 1), (1, 1024), "fast", "64x64"),     # to 512 (384) of 64x64, 2 per CU: 30.3 / 10.3 us
     (1536, 1536, 4096, (4096, 1), (1, 4096), "fast", "128x96k2"),  # 576 64x64 tiles (3 on some CUs): 128x96 keeps it
+    (512, 5120, 1024, (1024, 1), (1, 1024), "fast", "128x96k2"),   # ... also at K 1024 (64x64 won on two boxes, lost on one)
     (1024, 1024, 1536, (1536, 1), (1, 1536), "fast", "64x64"),     # two rounds of 64x32 at K 1536: 64x64 (11.2 vs 12.7)
     (1024, 1024, 2048, (2048, 1), (1, 2048), "fast", "64x32k4"),   # ... from K 2048 64x32 stays
     (2048, 1536, 8960, (8960, 1), (1536, 1), "fast", "128x128"),   # row-major b: 128x128 split in two
+    (4096, 3072, 4096, (4096, 1), (1, 4096), "fast", "256x256"),   # 768 128-tiles leave a lone last round: 192 of
+    (8192, 1536, 1536, (1536, 1), (1536, 1), "fast", "256x256"),   # 256x256 win (124.6 vs 132.8 us; 52.1 vs 56.7)
+    (3072, 1024, 4096, (4096, 1), (1024, 1), "fast", "64x64"),     # 768 64x64 tiles, 3 per CU: 46.4 vs 48.2 us
+    (256, 1024, 2048, (2048, 1), (1024, 1), "fast", "64x64"),      # 64x64 1 per CU over a split in two: 13.0 vs 19.0
+    (256, 11008, 8192, (8192, 1), (11008, 1), "fast", "128x128"),  # long K: a split in two beats 3 64x64 per CU
     (128, 1536, 1536, (1536, 1), (1536, 1), "fast", "64x64"),      # 128 rows, row-major b
     (2049, 1537, 8961, (8961, 1), (1, 8961), "fast", "128x128"),   # rows not 16-byte aligned: packed first
     (300, 1537, 8961, (8961, 1), (1, 8961), "reg", "128x128"),     # read in place (cheaper than a copy)
@@ -391,12 +397,16 @@ def test_k_split_only_where_it_pays(M, N, K, tile, splits):
 
 def test_workspace_holds_the_redo_list_where_it_is_deferred():
     """f16acc_workspace_size: one round of 256x256 tiles (4096^3) needs the
-    header alone (its flagged tiles are listed and redone by a second launch);
-    more rounds (8192^3: the persistent kernel redoes in place) and shapes
-    whose tiles fill the CUs on other tiles need nothing; a split-K plan needs
-    the header plus its partials."""
+    header alone (its flagged tiles are listed and redone by a second launch),
+    from 40 stages of K (K > 2496: 2560 lists, 2496 does not) up; shorter K
+    redoes in place (the second launch's fixed cost would pass 3 % of the
+    call); more rounds (8192^3: the persistent kernel redoes in place) and
+    shapes whose tiles fill the CUs on other tiles need nothing; a split-K
+    plan needs the header plus its partials."""
     n = ctypes.c_size_t()
     for (M, N, K, sbk, sbn), want in (((4096, 4096, 4096, 4096, 1), "header"), ((4096, 4096, 4096, 1, 4096), "header"),
+                                      ((4096, 4096, 2560, 4096, 1), "header"), ((4096, 4096, 2496, 4096, 1), "none"),
+                                      ((4096, 4096, 1024, 4096, 1), "none"),
                                       ((8192, 8192, 8192, 8192, 1), "none"), ((2048, 2048, 1536, 1, 1536), "none"),
                                       ((2048, 1536, 8960, 1536, 1), "split")):
         _lib.check(_lib.workspace_size(M, N, K, K, 1, sbk, sbn, 0, 0, ctypes.byref(n)))

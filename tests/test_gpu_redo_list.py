@@ -75,10 +75,10 @@ def _overflowing(M, N, K, rows, cols, seed):
 
 
 CASES = [  # M, N, K, row blocks, column blocks, b = w.t(), out dtype, bias
-    (4096, 4096, 1024, [3, 9, 17, 30], [0, 11, 22, 31], False, torch.float32, False),
-    (4096, 4096, 1024, [3, 9, 17, 30], [0, 11, 22, 31], True, torch.float16, True),
-    (3000, 3504, 520, [0, 11, 23], [1, 13, 27], True, torch.float32, True),   # ragged edge tiles flagged
-    (3000, 3504, 520, [0, 11, 23], [1, 13, 27], False, torch.float16, False),
+    (4096, 4096, 2560, [3, 9, 17, 30], [0, 11, 22, 31], False, torch.float32, False),
+    (4096, 4096, 2560, [3, 9, 17, 30], [0, 11, 22, 31], True, torch.float16, True),
+    (3000, 3504, 2600, [0, 11, 23], [1, 13, 27], True, torch.float32, True),   # ragged edge tiles flagged, ragged K
+    (3000, 3504, 2600, [0, 11, 23], [1, 13, 27], False, torch.float16, False),
 ]
 
 
@@ -121,8 +121,8 @@ def test_one_tile_grid_between_full_grids_on_one_workspace():
     equals the in-place redo, so no line keeps a stale length."""
     ws = _ws()
     tile = _lib.TILES.index("256x256")
-    big = _overflowing(4096, 4096, 512, [3, 17], [6, 25], 9)
-    small = _overflowing(256, 256, 256, [0], [1], 10)
+    big = _overflowing(4096, 4096, 2560, [3, 17], [6, 25], 9)
+    small = _overflowing(256, 256, 2560, [0], [1], 10)
     for a, b in (big, small, big):
         ga, gb = a.cuda(), b.cuda()
         M, K = a.shape
@@ -139,17 +139,14 @@ def test_one_tile_grid_between_full_grids_on_one_workspace():
 
 
 def test_every_tile_flagged_and_none_flagged():
-    """All 256 tiles of 4096 x 4096 x 256 listed (1024 quarters for the redo
+    """All 256 tiles of 4096 x 4096 x 2560 listed (1024 quarters for the redo
     launch's 256 workgroups), then a clean call on the same workspace: each
     equals the in-place redo."""
     M = N = 4096
-    K = 256
+    K = 2560
     a = torch.full((M, K), 100.0, dtype=torch.float16)
     b = torch.full((K, N), 30.0, dtype=torch.float16)
-    b[32:64] = -30.0  # chunk sums of +-96000 (inf in fp16), exact total per pair
-    b[160:192] = -30.0
-    b[96:128] = -30.0
-    b[224:256] = -30.0
+    b.view(K // 32, 32, N)[1::2] = -30.0  # chunk sums of +-96000 (inf in fp16), exact total per pair
     clean = rnd((M, K), 7).cuda()
     ga, gb = a.cuda(), b.cuda()
     ws = _ws()
@@ -174,7 +171,7 @@ def test_graph_replays_of_a_listing_call_match_eager():
     (the redo launch empties the list on every replay)."""
     from f16acc_amd import kernel
 
-    a, b = _overflowing(4096, 4096, 512, [5, 20], [2, 29], 8)
+    a, b = _overflowing(4096, 4096, 2560, [5, 20], [2, 29], 8)
     ga, gb = a.cuda(), b.cuda()
     want = kernel.mm(ga, gb, torch.float32)
     s = torch.cuda.Stream()

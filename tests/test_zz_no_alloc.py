@@ -104,22 +104,23 @@ def test_noalloc_equals_workspace_entry_on_two_calls_in_a_row():
 
 
 def test_noalloc_unsplit_problem_equals_plain_entry():
-    """A problem whose tiles fill the GPU takes no split (4096 x 4096 x 1024,
+    """A problem whose tiles fill the GPU takes no split (4096 x 4096 x 2560,
     one round of 256x256 tiles, fp16 out); its overflowing tiles are listed in
     the scratch's header and redone by a second launch.  Three calls in a row
     (overflow, clean, overflow) each equal f16acc_gemm, which redoes in place,
     bit for bit: the list is emptied after each call."""
-    a, b = rnd((4096, 1024), 85), rnd((1024, 4096), 86)
+    K = 2560
+    a, b = rnd((4096, K), 85), rnd((K, 4096), 86)
     a[512:640] = 120.0  # 128 rows x 128 columns whose chunk sums pass 65504
     b[:, 1024:1152] = 120.0
-    clean_a = rnd((4096, 1024), 87).cuda()
+    clean_a = rnd((4096, K), 87).cuda()
     a, b = a.cuda(), b.cuda()
     assert _split_bytes(a, b) == 0
     for x in (a, clean_a, a):
         c = torch.empty(4096, 4096, device="cuda", dtype=torch.float16)
         _call(_lib.gemm_noalloc, x, b, None, c, None)
         plain = torch.empty_like(c)
-        _lib.check(_lib.gemm(x.data_ptr(), b.data_ptr(), plain.data_ptr(), None, 4096, 4096, 1024, 1024, 1, 4096, 1,
+        _lib.check(_lib.gemm(x.data_ptr(), b.data_ptr(), plain.data_ptr(), None, 4096, 4096, K, K, 1, 4096, 1,
                              4096, 1, _lib.OUT_F16, 1, torch.cuda.current_stream().cuda_stream))
         torch.cuda.synchronize()
         assert torch.equal(c, plain)
