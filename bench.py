@@ -212,9 +212,9 @@ def sweep_tiles(names, rounds=5):
         ops["mm"] = lambda: f16acc_amd.mm(a, b, out_dtype)
         ops["hipblaslt"] = lambda: torch.mm(a, b)
         times = {k: [] for k in ops}
-        for _ in range(rounds):
-            for k, op in ops.items():
-                times[k].append(burst_time(op))
+        for r in range(rounds):
+            for k in round_order(list(ops), r):
+                times[k].append(burst_time(ops[k]))
         row = {"workload": name, "M": M, "N": N, "K": K, "b": layout, "table": tile_config(a, b)["tile"]}
         row.update({k: round(flops / statistics.median(v) / 1e12, 1) for k, v in times.items()})
         print(json.dumps(row), flush=True)
@@ -277,14 +277,8 @@ def table_check(tokens=(256, 1024, 4096), rounds=4):
                 ops.update({tile: (lambda x=tile: mm_tile(a, b, x)) for tile in tiles})
                 runs = {k: [] for k in ops}
                 names = list(ops)
-                for r in range(rounds):
-                    # interleaved, so clock drift falls on all alike; the order
-                    # rotates and reverses from round to round, since the op
-                    # timed first after another shape runs ~2-5 % slow (kernel
-                    # times keep falling for tens of ms after a switch)
-                    shift = r * len(names) // rounds
-                    order = names[shift:] + names[:shift]
-                    for k in (order[::-1] if r % 2 else order):
+                for r in range(rounds):  # interleaved, so clock drift falls on all alike
+                    for k in round_order(names, r):
                         runs[k].append(settled_time(ops[k]))
                 t = {k: statistics.median(v) for k, v in runs.items()}
                 best = min(tiles, key=lambda k: t[k])
@@ -329,9 +323,7 @@ def large_grid_check(rounds=3):
         names = list(ops)
         runs = {k: [] for k in ops}
         for r in range(rounds):
-            shift = r * len(names) // rounds
-            order = names[shift:] + names[:shift]
-            for k in (order[::-1] if r % 2 else order):
+            for k in round_order(names, r):
                 runs[k].append(settled_time(ops[k], burst_ms=25.0))
         t = {k: statistics.median(v) for k, v in runs.items()}
         best = min(cands, key=lambda k: t[k])
@@ -374,9 +366,7 @@ def small_grid_check(rounds=3):
         names = list(ops)
         runs = {k: [] for k in ops}
         for r in range(rounds):
-            shift = r * len(names) // rounds
-            order = names[shift:] + names[:shift]
-            for k in (order[::-1] if r % 2 else order):
+            for k in round_order(names, r):
                 runs[k].append(settled_time(ops[k], burst_ms=20.0))
         t = {k: statistics.median(v) for k, v in runs.items()}
         best = min(cands, key=lambda k: t[k])
@@ -388,6 +378,18 @@ def small_grid_check(rounds=3):
     print(json.dumps({"shapes": len(ratios), "pick_is_best": sum(r >= 0.999 for r in ratios),
                       "within_5pct": sum(r >= 0.95 for r in ratios), "within_10pct": sum(r >= 0.90 for r in ratios),
                       "worst_best_forced_over_pick": round(min(ratios), 3)}), flush=True)
+
+
+def round_order(names, r):
+    """The order ops are timed in round r: the list rotated by r, and
+    reversed in every other pass through the rotations, so over the rounds
+    each op is timed first as often as any other, within one (the op timed
+    first after another one runs ~2-5 % slow: kernel times keep falling for
+    tens of ms after a switch, and a fixed order charges that to one op)."""
+    n = len(names)
+    shift = r % n
+    order = list(names[shift:]) + list(names[:shift])
+    return order[::-1] if (r // n) % 2 else order
 
 
 def settled_time(op, burst_ms=40.0):
@@ -432,9 +434,9 @@ def shapes_report(names, rounds=4):
                "fp32acc": lambda: f16acc_amd.mm(a, b, out_dtype, chunked=False),
                "hipblaslt": lambda: torch.mm(a, b)}
         times = {k: [] for k in ops}
-        for _ in range(rounds):
-            for k, op in ops.items():
-                times[k].append(settled_time(op))
+        for r in range(rounds):
+            for k in round_order(list(ops), r):
+                times[k].append(settled_time(ops[k]))
         c = f16acc_amd.mm(a, b, out_dtype)
         ref = a.double() @ b.double()
         err = ((c.double() - ref).abs().max() / ref.abs().max()).item()
@@ -647,8 +649,9 @@ def twin_ab(lib_path, shapes, rounds, shipped="shipped", twin="twin"):
     """f16acc_gemm_ws (the entry mm uses: split-K where the table splits) of
     the shipped library against the same source built with a -D switch
     (lib_path, loaded here only), through the C ABI on the same inputs, timed
-    in interleaved settled bursts (median over rounds); both return the same
-    bits on these inputs.  Yields one record per shape."""
+    in interleaved settled bursts (median over rounds, the two taking turns at
+    going first); both return the same bits on these inputs.  Yields one
+    record per shape."""
     import ctypes
 
     from f16acc_amd import _lib
@@ -676,9 +679,9 @@ def twin_ab(lib_path, shapes, rounds, shipped="shipped", twin="twin"):
         torch.cuda.synchronize()
         same = bool(torch.equal(outs[shipped], outs[twin]))
         times = {k: [] for k in ops}
-        for _ in range(rounds):
-            for k, op in ops.items():
-                times[k].append(settled_time(op))
+        for r in range(rounds):
+            for k in round_order(list(ops), r):
+                times[k].append(settled_time(ops[k]))
         t = {k: statistics.median(v) for k, v in times.items()}
         yield {"workload": name, "M": M, "N": N, "K": K, "b": "row-major [K,N]" if layout == "row" else "w.t()",
                "out": "fp32" if out_dtype == torch.float32 else "fp16",

@@ -8,6 +8,7 @@ import re
 import subprocess
 import sys
 
+import pytest
 import torch
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -36,3 +37,18 @@ def test_more_than_one_gpu_exits_with_a_message():
                        text=True, timeout=300, cwd=ROOT)
     assert r.returncode == 2
     assert "one GPU" in r.stderr and '"metric"' not in r.stdout
+
+
+@pytest.mark.parametrize("n, rounds", [(2, 4), (2, 6), (3, 6), (7, 4), (8, 4)])
+def test_every_op_is_timed_first_equally_often(n, rounds):
+    """bench.round_order: each round times every op once, and over the
+    rounds each op goes first as often as any other (within one), so the
+    slow first burst after a switch is not charged to one op."""
+    names = [f"op{i}" for i in range(n)]
+    firsts = {k: 0 for k in names}
+    for r in range(rounds):
+        order = bench.round_order(names, r)
+        assert sorted(order) == sorted(names)
+        firsts[order[0]] += 1
+    counts = [firsts[k] for k in names]
+    assert max(counts) - min(counts) <= 1
