@@ -10,6 +10,8 @@ GPU, so the oracle and the kernel see identical bits.  Tolerances:
   * overflow closed forms: exact
 """
 
+import ctypes
+
 import pytest
 import torch
 
@@ -1261,3 +1263,37 @@ def test_ragged_round_row_cut_equals_single_grid(b_layout):
     wo[40:50, 127] = -29.0
     co = f16acc.mm(xo.cuda(), wo.cuda().t(), torch.float32)
     assert torch.all(co[300:310, 40:50] == 100.0) and torch.all(co[8500:8510, 40:50] == 100.0)
+
+
+@pytest.mark.parametrize("M, N, K, b_layout, tile, split", [
+    (256, 1024, 2048, "row", "64x64", False),     # a partial 64x64 round over a 128x128 K split
+    (3072, 1024, 4096, "t", "64x64", False),      # three 64x64 per CU over one 128x128 per CU
+    (4096, 3072, 1024, "t", "256x256", False),    # a lone last 128x128 round: 256x256, redo in place (short K)
+    (4096, 3072, 2560, "row", "256x256", False),  # ... from K 2560 the deferred redo list
+    (256, 11008, 8192, "row", "128x128", True),   # long K keeps the 128x128 K split
+])
+def test_partial_round_picks_match_oracle(M, N, K, b_layout, tile, split):
+    """mm on shapes the table prices by partial rounds (fp16 out): the pick,
+    its whole output against the same tile forced (bit for bit where mm does
+    not split K, within the tolerance where it does: the split reassociates
+    the FP32 chunk sums), and corner and middle blocks of the output against
+    the oracle on the same rows and columns (chunk sums are per element)."""
+    a = rnd((M, K), 7100 + K)
+    b = rnd((K, N), 7200 + N, 0.02)
+    ga = a.cuda()
+    gb = b.cuda() if b_layout == "row" else b.t().contiguous().cuda().t()
+    assert tile_config(ga, gb)["tile"] == tile
+    n = ctypes.c_size_t()
+    _lib.check(_lib.workspace_size(M, N, K, ga.stride(0), ga.stride(1), gb.stride(0), gb.stride(1), ga.data_ptr(),
+                                   gb.data_ptr(), ctypes.byref(n)))
+    assert (n.value > _lib.WS_HEADER) == split, n.value
+    c = f16acc.mm(ga, gb)
+    forced = f16acc.kernel.mm_tile(ga, gb, tile)
+    torch.cuda.synchronize()
+    if split:
+        _check_against_oracle(c, forced.cpu().float(), (M, N, K, "split vs forced"))
+    else:
+        assert torch.equal(c, forced), (M, N, K)
+    for r0, c0 in ((0, 0), (M - 128, N - 128), (M // 2 // 64 * 64, N // 2 // 64 * 64)):
+        ref = chunk32.mm(a[r0:r0 + 128], b[:, c0:c0 + 128], torch.float16, tile=(128, 128))
+        _check_against_oracle(c[r0:r0 + 128, c0:c0 + 128], ref, (M, N, K, r0, c0))
