@@ -109,9 +109,10 @@ int f16acc_gemm_bias(const void* a, const void* b, const void* bias, void* c, ui
  * bytes plus the split-K partials, or 0 when it needs none.  Shapes with
  * few output tiles (k/v projections, 2048 x 256) leave most CUs idle;
  * splitting K into chunk-aligned ranges fills them.  Shapes of at most one
- * round of 256x256 tiles (4096^3) use the header alone: their tiles that
- * overflow are listed there and redone by a second launch (see
- * f16acc_gemm_ws).
+ * round of 256x256 tiles and K > 2496 (4096^3) use the header alone: their
+ * tiles that overflow are listed there and redone by a second launch (see
+ * f16acc_gemm_ws); at shorter K that launch would cost more than the
+ * in-place redo it replaces.
  */
 int f16acc_workspace_size(int64_t M, int64_t N, int64_t K,
                           int64_t sam, int64_t sak, int64_t sbk, int64_t sbn,
@@ -128,9 +129,10 @@ int f16acc_workspace_size(int64_t M, int64_t N, int64_t K,
  *     workgroup per tile adds them in split order, flags the tile when the
  *     total is not finite and recomputes it over all of K with FP32
  *     accumulation (kernel.py:70-81), and stores it.
- *   - A problem of at most one round of 256x256 tiles runs as f16acc_gemm,
- *     except that a flagged tile is appended to the header's list instead of
- *     being redone by its own workgroup, and a second launch always follows:
+ *   - A problem of at most one round of 256x256 tiles and K > 2496 runs as
+ *     f16acc_gemm, except that a flagged tile is appended to the header's
+ *     list instead of being redone by its own workgroup, and a second launch
+ *     always follows:
  *     each flagged tile is recomputed in FP32 as four 128x128 quarters by
  *     four workgroups, and the launch's workgroups leave at once when the list
  *     is empty (the reference's separate _redo launch, kernel.py:75-81,
