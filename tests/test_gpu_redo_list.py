@@ -82,6 +82,30 @@ CASES = [  # M, N, K, row blocks, column blocks, b = w.t(), out dtype, bias
 ]
 
 
+def test_short_k_redoes_in_place_through_the_workspace_entry():
+    """Below 40 stages of K (K = 2496) a one-round 256x256 problem does not
+    list its flagged tiles: f16acc_gemm_ws redoes them in place, as
+    f16acc_gemm does, and leaves the header's counters at zero; at K = 2560
+    the same shape lists them.  Both equal f16acc_gemm bit for bit, with the
+    same single flagged tile."""
+    M = N = 4096
+    for K, listed in ((2496, False), (2560, True)):
+        a, b = _overflowing(M, N, K, [5], [7], 11)
+        ga, gb = a.cuda(), b.cuda()
+        assert _listed(M, N, K, ga, gb) == listed, K
+        ws = _ws()
+        c0 = torch.full((M, N), float("nan"), device="cuda", dtype=torch.float16)
+        c1 = torch.full_like(c0, float("nan"))
+        f0 = torch.zeros(16, 16, device="cuda", dtype=torch.uint8)
+        f1 = torch.zeros_like(f0)
+        _gemm(ga, gb, c0, None, f0)
+        _gemm(ga, gb, c1, None, f1, ws)
+        torch.cuda.synchronize()
+        assert {tuple(t) for t in f0.nonzero().tolist()} == {(2, 3)}, K
+        assert torch.equal(f1, f0) and torch.equal(c1, c0), K
+        assert _counters_zero(ws), K
+
+
 @pytest.mark.parametrize("M, N, K, rows, cols, b_t, out_dtype, biased", CASES)
 def test_deferred_redo_equals_redo_in_place(M, N, K, rows, cols, b_t, out_dtype, biased):
     a, b = _overflowing(M, N, K, rows, cols, 5)
