@@ -1297,3 +1297,44 @@ def test_partial_round_picks_match_oracle(M, N, K, b_layout, tile, split):
     for r0, c0 in ((0, 0), (M - 128, N - 128), (M // 2 // 64 * 64, N // 2 // 64 * 64)):
         ref = chunk32.mm(a[r0:r0 + 128], b[:, c0:c0 + 128], torch.float16, tile=(128, 128))
         _check_against_oracle(c[r0:r0 + 128, c0:c0 + 128], ref, (M, N, K, r0, c0))
+
+
+@pytest.mark.parametrize("case", range(30))
+def test_randomized_large_grids_through_the_table(case):
+    """Seeded random shapes of one round or more (M, N in 256..6144, K in
+    512..4096, a multiple of 8), b row-major or w.t(), fp16 out: mm as
+    planned (any tile, a ragged-round cut, a deferred redo launch, a K split)
+    against the pick forced alone -- bit for bit when the plan is one
+    unsplit launch of that tile -- and, on corner and middle blocks, against
+    the oracle on the same rows and columns.  Where mm packs an operand
+    first (a row-major b with N not a multiple of 8), the forced run may read
+    it in place on another tile, and the two are compared to the tolerance."""
+    import random
+
+    r = random.Random(9100 + case)
+    M, N, K = r.randint(256, 6144), r.randint(256, 6144), 8 * r.randint(64, 512)
+    b_layout = r.choice(["row", "t"])
+    what = (case, M, N, K, b_layout)
+    a = rnd((M, K), 9200 + case)
+    b = rnd((K, N), 9300 + case, 0.05)
+    ga = a.cuda()
+    gb = b.cuda() if b_layout == "row" else b.t().contiguous().cuda().t()
+    pick = tile_config(ga, gb)["tile"]
+    one_launch = False
+    if b_layout == "t" or N % 8 == 0:  # read as given: the plan below is the one mm runs
+        n, cut = ctypes.c_size_t(), ctypes.c_int64()
+        _lib.check(_lib.workspace_size(M, N, K, ga.stride(0), ga.stride(1), gb.stride(0), gb.stride(1),
+                                       ga.data_ptr(), gb.data_ptr(), ctypes.byref(n)))
+        _lib.check(_lib.tail_split(M, N, K, ga.stride(0), ga.stride(1), gb.stride(0), gb.stride(1), ga.data_ptr(),
+                                   gb.data_ptr(), ctypes.byref(cut)))
+        one_launch = n.value <= _lib.WS_HEADER and cut.value == 0
+    c = f16acc.mm(ga, gb)
+    forced = f16acc.kernel.mm_tile(ga, gb, pick)
+    torch.cuda.synchronize()
+    if one_launch:
+        assert torch.equal(c, forced), (what, pick)
+    else:
+        _check_against_oracle(c, forced.cpu().float(), (what, pick))
+    for r0, c0 in ((0, 0), (M - 96, N - 96), (M // 2, N // 2)):
+        ref = chunk32.mm(a[r0:r0 + 96], b[:, c0:c0 + 96], torch.float16, tile=(96, 96))
+        _check_against_oracle(c[r0:r0 + 96, c0:c0 + 96], ref, (what, pick, r0, c0))
