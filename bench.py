@@ -31,7 +31,9 @@ redoes flagged tiles in a split-K pass instead of in the same workgroup;
 --workload table_check times the per-shape table against every forced tile on
 llama-2-7B, llama-3-8B and Qwen2.5-7B layer shapes; --workload small_grid_check
 times its small-grid picks (K-group tiles, 64x64) against the other candidates,
---workload large_grid_check its picks on grids of a round or more; --tile-calls runs every tile
+--workload large_grid_check its picks on grids of a round or more, --workload
+estimate_ab the picks its partial-round estimates changed against the picks
+before them; --tile-calls runs every tile
 untimed for rocprofv3 counter passes.
 """
 
@@ -716,6 +718,52 @@ PERSISTENT_SHAPES = (("qwen_lm_head", 2048, 151936, 1536, "t", torch.float16),
                      ("llama2_lm_head_4096tok", 4096, 32000, 4096, "t", torch.float16))
 
 
+# Shapes whose plan the partial-round estimates of the tile table changed,
+# with the tile the table picked before them (M, N, K, b layout, old pick).
+ESTIMATE_SHAPES = ((4096, 3072, 4096, "row", "128x128"), (4096, 3072, 4096, "t", "128x128"),
+                   (8192, 1536, 1536, "row", "128x128"), (5888, 9216, 4096, "row", "128x128"),
+                   (256, 1024, 2048, "row", "128x128"), (1024, 1024, 2048, "row", "128x128"),
+                   (4096, 512, 2048, "row", "128x128"), (256, 4096, 2560, "row", "128x128"),
+                   (3072, 1024, 4096, "row", "128x128"), (3072, 1024, 4096, "t", "128x128"),
+                   (2048, 1536, 3072, "row", "128x128"), (768, 4096, 3072, "t", "128x128"),
+                   (256, 11008, 8192, "row", "128x128"), (512, 6144, 14336, "row", "128x128"))
+
+
+def estimate_ab(rounds=4):
+    """mm as shipped against the plan the table made before it priced
+    partial rounds of 128x128 (a lone last round) and 64x64 (a single round
+    of three or fewer workgroups per CU): that pick forced through
+    f16acc_gemm_tile_ws, which plans its K split as before and makes no
+    ragged-round cut.  Per-call times in settled bursts, median of rounds
+    whose order alternates; fp16 out.  pct < 0: the new plan is faster."""
+    import ctypes
+
+    import f16acc_amd
+    from f16acc_amd import _lib
+    from f16acc_amd.kernel import tile_config
+
+    ws = torch.empty((32 << 20) + _lib.WS_HEADER, dtype=torch.uint8, device="cuda")
+    ws[:_lib.WS_HEADER].zero_()
+    for M, N, K, layout, old in ESTIMATE_SHAPES:
+        _, _, a, b = make_inputs(M, N, K, layout)
+        c_old = torch.empty(M, N, device="cuda", dtype=torch.float16)
+        stream = torch.cuda.current_stream().cuda_stream
+        args = (a.data_ptr(), b.data_ptr(), c_old.data_ptr(), None, M, N, K, a.stride(0), a.stride(1), b.stride(0),
+                b.stride(1), c_old.stride(0), c_old.stride(1), _lib.OUT_F16, 1, stream, _lib.TILES.index(old),
+                ws.data_ptr(), ws.numel())
+        ops = {"new": lambda: f16acc_amd.mm(a, b), "old": lambda: _lib.check(_lib.gemm_tile_ws(*args))}
+        times = {k: [] for k in ops}
+        for r in range(rounds):
+            for k in round_order(list(ops), r):
+                times[k].append(settled_time(ops[k]))
+        t = {k: statistics.median(v) * 1e6 for k, v in times.items()}
+        print(json.dumps({"M": M, "N": N, "K": K, "b": layout, "pick_new": tile_config(a, b)["tile"], "pick_old": old,
+                          "us_new": round(t["new"], 2), "us_old": round(t["old"], 2),
+                          "pct": round((t["new"] / t["old"] - 1) * 100, 2)}), flush=True)
+        del a, b, c_old
+        torch.cuda.empty_cache()
+
+
 def persistent_ab(rounds=5):
     """Multi-round shapes on the persistent 256x256 kernel (the shipped
     library) against the one-tile-per-workgroup grid
@@ -851,7 +899,8 @@ def main():
     ap.add_argument("--workload", default="gemm4096",
                     choices=sorted(WORKLOADS) + ["copy", "overflow", "overflow_split_redo", "qwen2_prefill",
                                                  "redo_overhead", "persistent_ab", "shapes",
-                                                 "table_check", "small_grid_check", "large_grid_check"])
+                                                 "table_check", "small_grid_check", "large_grid_check",
+                                                 "estimate_ab"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and oracle comparison")
     ap.add_argument("--preheat", type=float, default=PREHEAT_S,
                     help="seconds of back-to-back calls before the warm-up steps (0 for counter runs)")
@@ -876,6 +925,8 @@ def main():
         return small_grid_check()
     if args.workload == "large_grid_check":
         return large_grid_check()
+    if args.workload == "estimate_ab":
+        return estimate_ab()
     if args.workload == "shapes":
         return shapes_report(list(WORKLOADS))
     if args.workload == "overflow":
